@@ -1,0 +1,106 @@
+// Embedding gather for gfx950: out[t, :] = weight[ids[t], :], a bit-exact row copy.
+//
+// Reference: torch.nn.Embedding.forward as called by emberserve/model/qwen2.py:182 and
+// deepseek.py:205 (F.embedding without max_norm / padding_idx effects on the forward).
+//
+// Work mapping: one wave64 per token. The row is copied in 16-byte units when row bytes,
+// strides and base pointers allow it (else 8/4/2/1-byte units); each lane keeps U units in
+// flight, so a 8 KiB row (hidden 4096, bf16) is one round of 8 dwordx4 loads per lane.
+// An id outside [0, vocab) writes a zero row and sets EMBER_ERR_EMBED_ID; it never reads
+// outside the table.
+#include "ember_common.h"
+
+namespace ember {
+namespace {
+
+template <int VB>
+struct Unit;
+template <>
+struct Unit<16> {
+  using type = Pack<uint32_t, 4>;
+};
+template <>
+struct Unit<8> {
+  using type = Pack<uint32_t, 2>;
+};
+template <>
+struct Unit<4> {
+  using type = uint32_t;
+};
+template <>
+struct Unit<2> {
+  using type = uint16_t;
+};
+template <>
+struct Unit<1> {
+  using type = uint8_t;
+};
+
+template <int VB, int U>
+__global__ void __launch_bounds__(256)
+k_embedding(const int64_t* __restrict__ ids, int64_t ntok, const uint8_t* __restrict__ w, int64_t vocab,
+            int64_t w_stride_bytes, uint8_t* __restrict__ out, int64_t out_stride_bytes, int nunits,
+            uint32_t* __restrict__ err) {
+  using V = typename Unit<VB>::type;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (tok >= ntok) return;
+  const int64_t id = ids[tok];
+  V* dst = reinterpret_cast<V*>(out + tok * out_stride_bytes);
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(err, EMBER_ERR_EMBED_ID);
+    V zero{};
+    for (int i = lane; i < nunits; i += kWave) dst[i] = zero;
+    return;
+  }
+  const V* src = reinterpret_cast<const V*>(w + id * w_stride_bytes);
+  for (int base = 0; base < nunits; base += kWave * U) {
+    V buf[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) buf[k] = src[min(base + lane + k * kWave, nunits - 1)];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + lane + k * kWave;
+      if (i < nunits) dst[i] = buf[k];
+    }
+  }
+}
+
+template <int VB>
+int launch_vb(const int64_t* ids, int64_t ntok, const void* w, int64_t vocab, int64_t wsb, void* out,
+              int64_t osb, int64_t row_bytes, uint32_t* err, hipStream_t stream) {
+  const int64_t nunits = row_bytes / VB;
+  const int64_t grid = cdiv(ntok, 4);
+  if (grid > 0x7fffffffLL || nunits > 0x7fffffffLL) return EMBER_EINVAL;
+  hipLaunchKernelGGL((k_embedding<VB, 8>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, ids, ntok,
+                     static_cast<const uint8_t*>(w), vocab, wsb, static_cast<uint8_t*>(out), osb,
+                     static_cast<int>(nunits), err);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" int ember_embedding(const int64_t* ids, int64_t num_tokens, const void* weight, int64_t vocab,
+                               int64_t hidden, int64_t weight_row_stride, void* out, int64_t out_row_stride,
+                               int64_t elem_bytes, void* stream) {
+  using namespace ember;
+  if (num_tokens < 0 || hidden <= 0 || vocab < 0) return EMBER_EINVAL;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return EMBER_EINVAL;
+  if (num_tokens == 0) return EMBER_OK;
+  if (ids == nullptr || weight == nullptr || out == nullptr) return EMBER_EINVAL;
+  uint32_t* err = device_error_word();
+  if (err == nullptr) return EMBER_ENODEV;
+  const int64_t row_bytes = hidden * elem_bytes;
+  const int64_t wsb = weight_row_stride * elem_bytes;
+  const int64_t osb = out_row_stride * elem_bytes;
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out) |
+                         static_cast<uintptr_t>(row_bytes) | static_cast<uintptr_t>(wsb) |
+                         static_cast<uintptr_t>(osb);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((bits & 15u) == 0) return launch_vb<16>(ids, num_tokens, weight, vocab, wsb, out, osb, row_bytes, err, s);
+  if ((bits & 7u) == 0) return launch_vb<8>(ids, num_tokens, weight, vocab, wsb, out, osb, row_bytes, err, s);
+  if ((bits & 3u) == 0) return launch_vb<4>(ids, num_tokens, weight, vocab, wsb, out, osb, row_bytes, err, s);
+  if ((bits & 1u) == 0) return launch_vb<2>(ids, num_tokens, weight, vocab, wsb, out, osb, row_bytes, err, s);
+  return launch_vb<1>(ids, num_tokens, weight, vocab, wsb, out, osb, row_bytes, err, s);
+}

@@ -1,0 +1,159 @@
+// Device-side building blocks shared by the gfx950 kernels of libember_ops.so.
+//
+// Conventions of every kernel in this library:
+//  * storage dtypes fp32 / fp16 / bf16, all arithmetic in fp32;
+//  * "round_to<T>(v)" is the round-to-nearest-even cast to T and back, i.e. the rounding a
+//    PyTorch eager op applies when it writes a half-precision tensor;
+//  * the library is compiled with -ffp-contract=off, so a*b+c is two rounded operations,
+//    as in the reference's separate element-wise tensor ops;
+//  * 16-byte (dwordx4) accesses: a "Pack<T, VEC>" is VEC elements = 16 bytes for the
+//    vector kernels (VEC = 8 for fp16/bf16, 4 for fp32);
+//  * reductions stay inside a wavefront (DPP row ops, one ds_swizzle, v_readlane) and
+//    touch LDS only to combine the waves of a multi-wave row team.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ember_ops.h"
+
+namespace ember {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- dtype conversion
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }  // RNE
+
+template <typename T>
+__device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// ---------------------------------------------------------------- 16-byte packs
+
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Pack {
+  T v[N];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_pack(const T* p) {
+  return *reinterpret_cast<const Pack<T, N>*>(p);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_pack(T* p, const Pack<T, N>& v) {
+  *reinterpret_cast<Pack<T, N>*>(p) = v;
+}
+
+// Loads N consecutive values of type T (16-byte aligned when N * sizeof(T) >= 16) as fp32.
+template <typename T, int N>
+__device__ __forceinline__ void load_vals(const T* p, float (&out)[N]) {
+  constexpr int kPer = 16 / sizeof(T);
+  if constexpr (N < kPer) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = to_f32(p[e]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < N; h += kPer) {
+      Pack<T, kPer> q = load_pack<T, kPer>(p + h);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) out[h + e] = to_f32(q.v[e]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- wave reductions
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xF, 0xF, false));
+}
+
+// ds_swizzle in bit-mask mode: lane i reads lane (i ^ 16) within its 32-lane half.
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64). Every lane of a group must
+// be active; lanes only read lanes of their own group, so other groups may be inactive.
+// All lanes of a group return the same bits (the pairing order is symmetric).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  if constexpr (W >= 2) v += dpp_f32<kDppQuadSwap1>(v);
+  if constexpr (W >= 4) v += dpp_f32<kDppQuadSwap2>(v);
+  if constexpr (W >= 8) v += dpp_f32<kDppRowHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_f32<kDppRowMirror>(v);
+  if constexpr (W >= 32) v += swizzle_xor16(v);
+  if constexpr (W >= 64) {
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    v = lo + hi;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- integer division
+
+// Division of a uint32 n < 2^31 by a runtime-constant d >= 1 with one mul-hi
+// (Granlund-Montgomery, round-up variant).
+struct FastDiv {
+  uint32_t d;
+  uint32_t m;
+  uint32_t s;
+
+  __host__ static FastDiv make(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    f.s = s;
+    f.m = static_cast<uint32_t>(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (__umulhi(n, m) + n) >> s;
+  }
+};
+
+// ---------------------------------------------------------------- host helpers
+
+__host__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__host__ inline int dtype_size(int dtype) {
+  switch (dtype) {
+    case EMBER_F32: return 4;
+    case EMBER_F16: return 2;
+    case EMBER_BF16: return 2;
+    default: return 0;
+  }
+}
+
+__host__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+__host__ inline int pow2_ceil(int64_t v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+// Returns the device address of this library's error word on the current device.
+__host__ uint32_t* device_error_word();
+
+__host__ inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ELAUNCH;
+}
+
+}  // namespace ember

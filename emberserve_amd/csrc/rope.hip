@@ -1,0 +1,557 @@
+// Neox rotary embedding, Qwen3 QK-RMSNorm + rope, and the MLA latent norm + decoupled
+// rope, for gfx950.
+//
+// Rope (emberserve/model/ops.py:66-81, ops_triton.py:37-70), for i < D/2:
+//   o[i]       = round(x[i] * c[i] - x[i + D/2] * s[i])
+//   o[i + D/2] = round(x[i + D/2] * c[i] + x[i] * s[i])
+// c, s = cos/sin_table[pos][i] (fp32 tables whose halves are equal), each product and the
+// sum rounded separately in fp32 (the library builds with -ffp-contract=off).
+//
+// QK-norm (qwen2.py:95-101): each head row is first RMS-normalised exactly as
+// ember_rmsnorm does (y = round(round(x * inv) * w)) and the rope is applied to y; the
+// fused kernel keeps y in registers instead of writing and re-reading it.
+//
+// Layout: q [T, Hq, D] and k [T, Hk, D] with unit stride inside a head, any token/head
+// strides (views into the fused qkv projection output). Updates are in place.
+//
+// Work mapping (rope and qk-norm): J = D / (2 * VEC) lanes own one head row; lane j holds
+// the 16-byte pack j of the first half and pack j of the second half, i.e. exactly the
+// pairs it rotates, so no lane exchange is needed. A lane processes G heads of one token
+// (loads of all G heads are issued before any arithmetic) and reads that token's c/s
+// packs once for all of them. The qk-norm sum of squares is a J-lane DPP reduction.
+#include "ember_common.h"
+
+namespace ember {
+namespace {
+
+template <typename T, typename WT, int VEC, int J, int G, bool NORM>
+__global__ void __launch_bounds__(256)
+k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, int64_t kts, int64_t khs,
+       int hk, int half, const WT* __restrict__ qw, const WT* __restrict__ kw, float eps,
+       const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
+       const int64_t* __restrict__ pos, uint32_t ntok, uint32_t ngroups, FastDiv gdiv,
+       uint32_t* __restrict__ err) {
+  const uint32_t gt = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t j = gt % J;
+  const uint32_t rowid = gt / J;
+  const uint32_t tok = gdiv.div(rowid);
+  if (tok >= ntok) return;  // whole J-lane groups leave together
+  const uint32_t hg = rowid - tok * ngroups;
+  const int64_t p = pos[tok];
+  if (p < 0 || p >= trows) {
+    if (j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+    return;
+  }
+  const int nh = hq + hk;
+  const int64_t off = static_cast<int64_t>(j) * VEC;
+
+  Pack<T, VEC> x1[G];
+  Pack<T, VEC> x2[G];
+  T* ptr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int h = min(static_cast<int>(hg) * G + g, nh - 1);
+    ptr[g] = (h < hq ? q + tok * qts + h * qhs : k + tok * kts + (h - hq) * khs) + off;
+    x1[g] = load_pack<T, VEC>(ptr[g]);
+    x2[g] = load_pack<T, VEC>(ptr[g] + half);
+  }
+  float c[VEC];
+  float s[VEC];
+  load_vals<float, VEC>(cos_t + p * tstride + off, c);
+  load_vals<float, VEC>(sin_t + p * tstride + off, s);
+  float wq1[VEC], wq2[VEC], wk1[VEC], wk2[VEC];
+  if constexpr (NORM) {
+    load_vals<WT, VEC>(qw + off, wq1);
+    load_vals<WT, VEC>(qw + half + off, wq2);
+    load_vals<WT, VEC>(kw + off, wk1);
+    load_vals<WT, VEC>(kw + half + off, wk2);
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int h = static_cast<int>(hg) * G + g;
+    if (h < nh) {  // uniform across the J lanes of the head
+      float f1[VEC];
+      float f2[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        f1[e] = to_f32(x1[g].v[e]);
+        f2[e] = to_f32(x2[g].v[e]);
+      }
+      if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) ss += f1[e] * f1[e] + f2[e] * f2[e];
+        const float tot = group_sum<J>(ss);
+        const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+        const bool isq = h < hq;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          f1[e] = round_to<T>(round_to<T>(f1[e] * inv) * (isq ? wq1[e] : wk1[e]));
+          f2[e] = round_to<T>(round_to<T>(f2[e] * inv) * (isq ? wq2[e] : wk2[e]));
+        }
+      }
+      Pack<T, VEC> o1;
+      Pack<T, VEC> o2;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        o1.v[e] = from_f32<T>(f1[e] * c[e] - f2[e] * s[e]);
+        o2.v[e] = from_f32<T>(f2[e] * c[e] + f1[e] * s[e]);
+      }
+      store_pack<T, VEC>(ptr[g], o1);
+      store_pack<T, VEC>(ptr[g] + half, o2);
+    }
+  }
+}
+
+// Any head_dim, any alignment: one wave per (token, head), scalar accesses, loops over the
+// half dimension (the norm variant reads the row twice, the second time from cache).
+template <typename T, typename WT, bool NORM>
+__global__ void __launch_bounds__(256)
+k_rope_any(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, int64_t kts, int64_t khs,
+           int hk, int half, const WT* __restrict__ qw, const WT* __restrict__ kw, float eps,
+           const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
+           const int64_t* __restrict__ pos, int64_t ntok, uint32_t* __restrict__ err) {
+  const int64_t rowid = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int nh = hq + hk;
+  const int64_t tok = rowid / nh;
+  const int h = static_cast<int>(rowid - tok * nh);
+  if (tok >= ntok) return;
+  const int64_t p = pos[tok];
+  if (p < 0 || p >= trows) {
+    if (lane == 0 && h == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+    return;
+  }
+  T* ptr = h < hq ? q + tok * qts + h * qhs : k + tok * kts + (h - hq) * khs;
+  const WT* w = h < hq ? qw : kw;
+  float inv = 1.f;
+  if constexpr (NORM) {
+    float ss = 0.f;
+    for (int i = lane; i < 2 * half; i += kWave) {
+      const float f = to_f32(ptr[i]);
+      ss += f * f;
+    }
+    const float tot = group_sum<kWave>(ss);
+    inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+  }
+  for (int i = lane; i < half; i += kWave) {
+    float f1 = to_f32(ptr[i]);
+    float f2 = to_f32(ptr[half + i]);
+    if constexpr (NORM) {
+      f1 = round_to<T>(round_to<T>(f1 * inv) * to_f32(w[i]));
+      f2 = round_to<T>(round_to<T>(f2 * inv) * to_f32(w[half + i]));
+    }
+    const float c = cos_t[p * tstride + i];
+    const float s = sin_t[p * tstride + i];
+    ptr[i] = from_f32<T>(f1 * c - f2 * s);
+    ptr[half + i] = from_f32<T>(f2 * c + f1 * s);
+  }
+}
+
+struct RopeArgs {
+  void* q;
+  int64_t qts, qhs, hq;
+  void* k;
+  int64_t kts, khs, hk;
+  int64_t head_dim;
+  const void* qw;
+  const void* kw;
+  float eps;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t trows, tstride;
+  const int64_t* pos;
+  int64_t ntok;
+  hipStream_t stream;
+  uint32_t* err;
+};
+
+template <typename T, typename WT, int VEC, int J, int G, bool NORM>
+int launch_vec(const RopeArgs& a) {
+  const int64_t nh = a.hq + a.hk;
+  const int64_t ngroups = cdiv(nh, G);
+  const int64_t threads = a.ntok * ngroups * J;
+  if (threads > 0x7fffffffLL) return EMBER_EINVAL;  // FastDiv needs indices < 2^31
+  const int64_t grid = cdiv(threads, 256);
+  hipLaunchKernelGGL((k_rope<T, WT, VEC, J, G, NORM>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+                     static_cast<T*>(a.q), a.qts, a.qhs, static_cast<int>(a.hq), static_cast<T*>(a.k), a.kts,
+                     a.khs, static_cast<int>(a.hk), static_cast<int>(a.head_dim / 2),
+                     static_cast<const WT*>(a.qw), static_cast<const WT*>(a.kw), a.eps, a.cos_t, a.sin_t,
+                     a.trows, a.tstride, a.pos, static_cast<uint32_t>(a.ntok), static_cast<uint32_t>(ngroups),
+                     FastDiv::make(static_cast<uint32_t>(ngroups)), a.err);
+  return launch_status();
+}
+
+template <typename T, typename WT, int VEC, int J, bool NORM>
+int launch_g(const RopeArgs& a) {
+  // Heads per lane: as many as keep >= 2^17 lanes busy (up to 4), so large batches get
+  // more loads in flight per lane and fewer c/s table reads.
+  const int64_t nh = a.hq + a.hk;
+  if (a.ntok * cdiv(nh, 4) * J >= 131072) return launch_vec<T, WT, VEC, J, 4, NORM>(a);
+  if (a.ntok * cdiv(nh, 2) * J >= 131072) return launch_vec<T, WT, VEC, J, 2, NORM>(a);
+  return launch_vec<T, WT, VEC, J, 1, NORM>(a);
+}
+
+template <typename T, typename WT, bool NORM>
+int launch_typed(const RopeArgs& a) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t half = a.head_dim / 2;
+  const int64_t j = half / VEC;
+  const bool have_k = a.hk > 0;
+  bool vec_ok = half % VEC == 0 && (j & (j - 1)) == 0 && j >= 1 && j <= 32 && aligned16(a.q) &&
+                a.qts % VEC == 0 && a.qhs % VEC == 0 && aligned16(a.cos_t) && aligned16(a.sin_t) &&
+                a.tstride % 4 == 0;
+  if (have_k) vec_ok = vec_ok && aligned16(a.k) && a.kts % VEC == 0 && a.khs % VEC == 0;
+  if (NORM) vec_ok = vec_ok && aligned16(a.qw) && (!have_k || aligned16(a.kw));
+  if (vec_ok) {
+    switch (j) {
+      case 1: return launch_g<T, WT, VEC, 1, NORM>(a);
+      case 2: return launch_g<T, WT, VEC, 2, NORM>(a);
+      case 4: return launch_g<T, WT, VEC, 4, NORM>(a);
+      case 8: return launch_g<T, WT, VEC, 8, NORM>(a);
+      case 16: return launch_g<T, WT, VEC, 16, NORM>(a);
+      case 32: return launch_g<T, WT, VEC, 32, NORM>(a);
+      default: break;
+    }
+  }
+  const int64_t rows = a.ntok * (a.hq + a.hk);
+  const int64_t grid = cdiv(rows, 4);
+  if (grid > 0x7fffffffLL) return EMBER_EINVAL;
+  hipLaunchKernelGGL((k_rope_any<T, WT, NORM>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+                     static_cast<T*>(a.q), a.qts, a.qhs, static_cast<int>(a.hq), static_cast<T*>(a.k), a.kts,
+                     a.khs, static_cast<int>(a.hk), static_cast<int>(half), static_cast<const WT*>(a.qw),
+                     static_cast<const WT*>(a.kw), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
+                     a.err);
+  return launch_status();
+}
+
+int check_rope_args(const RopeArgs& a) {
+  if (a.ntok < 0 || a.hq < 0 || a.hk < 0 || a.head_dim <= 0 || a.head_dim % 2 != 0) return EMBER_EINVAL;
+  if (a.head_dim > 4096 || a.hq + a.hk > 0x7fffffff || a.trows < 0 || a.tstride < a.head_dim / 2)
+    return EMBER_EINVAL;
+  if (a.ntok == 0 || a.hq + a.hk == 0) return -1;  // nothing to do
+  if (a.cos_t == nullptr || a.sin_t == nullptr || a.pos == nullptr) return EMBER_EINVAL;
+  if (a.hq > 0 && a.q == nullptr) return EMBER_EINVAL;
+  if (a.hk > 0 && a.k == nullptr) return EMBER_EINVAL;
+  return EMBER_OK;
+}
+
+// ---------------------------------------------------------------- MLA latent path
+//
+// deepseek.py:124-133 with the rope permutation folded into the weights: per token,
+//   latent[:R] = rmsnorm(c, w), latent[R:R+Dr] = rope(k_pe), q_pe[h] = rope(q_pe[h]).
+// One wave64 per token. The R-wide latent row is held as NVC packs per lane and reduced
+// over the whole wave; the (H + 1) rope head rows (H query heads and the single key head)
+// are J-lane items, two items per lane per round with all their loads issued first.
+
+template <typename T, typename WT, int VEC, int J, int NVC>
+__global__ void __launch_bounds__(256)
+k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
+      int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
+      const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
+      const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts,
+      uint32_t* __restrict__ err) {
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (tok >= ntok) return;
+  const int ncv = R / VEC;
+
+  // Latent row: issue its loads first.
+  Pack<T, VEC> cv[NVC];
+  float wv[NVC][VEC];
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) {
+    const int vi = min(lane + i * kWave, ncv - 1);
+    cv[i] = load_pack<T, VEC>(c + tok * cts + static_cast<int64_t>(vi) * VEC);
+    load_vals<WT, VEC>(w + static_cast<int64_t>(vi) * VEC, wv[i]);
+  }
+  const int64_t p = pos[tok];
+  const bool bad = p < 0 || p >= trows;
+  const int64_t pc = bad ? 0 : p;
+
+  float v[NVC][VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) {
+    const bool ok = lane + i * kWave < ncv;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float f = ok ? to_f32(cv[i].v[e]) : 0.f;
+      v[i][e] = f;
+      ss += f * f;
+    }
+  }
+  const float tot = group_sum<kWave>(ss);
+  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) {
+    const int vi = lane + i * kWave;
+    if (vi < ncv) {
+      Pack<T, VEC> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * wv[i][e]);
+      store_pack<T, VEC>(lat + tok * lts + static_cast<int64_t>(vi) * VEC, o);
+    }
+  }
+
+  if (bad && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+  const int items = (H + 1) * J;
+  for (int base = 0; base < items; base += 2 * kWave) {
+    Pack<T, VEC> a1[2];
+    Pack<T, VEC> a2[2];
+    float cc[2][VEC];
+    float sn[2][VEC];
+    const T* src[2];
+    T* dst[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = min(base + lane + u * kWave, items - 1);
+      const int head = it / J;
+      const int64_t off = static_cast<int64_t>(it % J) * VEC;
+      if (head < H) {
+        T* pq = qpe + tok * qts + static_cast<int64_t>(head) * qhs + off;
+        src[u] = pq;
+        dst[u] = pq;
+      } else {
+        src[u] = kpe + tok * kts + off;
+        dst[u] = lat + tok * lts + R + off;
+      }
+      a1[u] = load_pack<T, VEC>(src[u]);
+      a2[u] = load_pack<T, VEC>(src[u] + half);
+      load_vals<float, VEC>(cos_t + pc * tstride + off, cc[u]);
+      load_vals<float, VEC>(sin_t + pc * tstride + off, sn[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int it = base + lane + u * kWave;
+      if (it < items) {
+        Pack<T, VEC> o1;
+        Pack<T, VEC> o2;
+        if (!bad) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float f1 = to_f32(a1[u].v[e]);
+            const float f2 = to_f32(a2[u].v[e]);
+            o1.v[e] = from_f32<T>(f1 * cc[u][e] - f2 * sn[u][e]);
+            o2.v[e] = from_f32<T>(f2 * cc[u][e] + f1 * sn[u][e]);
+          }
+          store_pack<T, VEC>(dst[u], o1);
+          store_pack<T, VEC>(dst[u] + half, o2);
+        } else if (it / J >= H) {  // bad position: q_pe untouched, latent key slot zeroed
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            o1.v[e] = from_f32<T>(0.f);
+          }
+          store_pack<T, VEC>(dst[u], o1);
+          store_pack<T, VEC>(dst[u] + half, o1);
+        }
+      }
+    }
+  }
+}
+
+// Any shape, any alignment: one wave per token, scalar accesses.
+template <typename T, typename WT>
+__global__ void __launch_bounds__(256)
+k_mla_any(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts,
+          T* __restrict__ qpe, int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
+          const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
+          const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts,
+          uint32_t* __restrict__ err) {
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (tok >= ntok) return;
+  float ss = 0.f;
+  for (int i = lane; i < R; i += kWave) {
+    const float f = to_f32(c[tok * cts + i]);
+    ss += f * f;
+  }
+  const float tot = group_sum<kWave>(ss);
+  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+  for (int i = lane; i < R; i += kWave)
+    lat[tok * lts + i] = from_f32<T>(round_to<T>(to_f32(c[tok * cts + i]) * inv) * to_f32(w[i]));
+  const int64_t p = pos[tok];
+  if (p < 0 || p >= trows) {
+    if (lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+    for (int i = lane; i < 2 * half; i += kWave) lat[tok * lts + R + i] = from_f32<T>(0.f);
+    return;
+  }
+  for (int it = lane; it < (H + 1) * half; it += kWave) {
+    const int head = it / half;
+    const int i = it - head * half;
+    const T* src = head < H ? qpe + tok * qts + static_cast<int64_t>(head) * qhs : kpe + tok * kts;
+    T* dst = head < H ? qpe + tok * qts + static_cast<int64_t>(head) * qhs : lat + tok * lts + R;
+    const float f1 = to_f32(src[i]);
+    const float f2 = to_f32(src[half + i]);
+    const float cv = cos_t[p * tstride + i];
+    const float sv = sin_t[p * tstride + i];
+    dst[i] = from_f32<T>(f1 * cv - f2 * sv);
+    dst[half + i] = from_f32<T>(f2 * cv + f1 * sv);
+  }
+}
+
+struct MlaArgs {
+  const void* c;
+  int64_t cts, R;
+  const void* kpe;
+  int64_t kts;
+  void* qpe;
+  int64_t qts, qhs, H, rope_dim;
+  const void* w;
+  float eps;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t trows, tstride;
+  const int64_t* pos;
+  int64_t ntok;
+  void* lat;
+  int64_t lts;
+  hipStream_t stream;
+  uint32_t* err;
+};
+
+template <typename T, typename WT, int VEC, int J, int NVC>
+int launch_mla_vec(const MlaArgs& a) {
+  const int64_t grid = cdiv(a.ntok, 4);
+  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+                     static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
+                     static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2),
+                     static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
+                     static_cast<T*>(a.lat), a.lts, a.err);
+  return launch_status();
+}
+
+template <typename T, typename WT, int VEC, int J>
+int launch_mla_nvc(const MlaArgs& a, int nvc) {
+  switch (nvc) {
+    case 1: return launch_mla_vec<T, WT, VEC, J, 1>(a);
+    case 2: return launch_mla_vec<T, WT, VEC, J, 2>(a);
+    case 4: return launch_mla_vec<T, WT, VEC, J, 4>(a);
+    case 8: return launch_mla_vec<T, WT, VEC, J, 8>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
+template <typename T, typename WT>
+int launch_mla_typed(const MlaArgs& a) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t half = a.rope_dim / 2;
+  const int64_t j = half / VEC;
+  const int64_t ncv = a.R / VEC;
+  const bool vec_ok = a.R % VEC == 0 && ncv <= 8 * kWave && half % VEC == 0 && (j & (j - 1)) == 0 && j >= 1 &&
+                      j <= 16 && aligned16(a.c) && aligned16(a.kpe) && aligned16(a.qpe) && aligned16(a.lat) &&
+                      aligned16(a.w) && aligned16(a.cos_t) && aligned16(a.sin_t) && a.tstride % 4 == 0 &&
+                      a.cts % VEC == 0 && a.kts % VEC == 0 && a.qts % VEC == 0 && a.qhs % VEC == 0 &&
+                      a.lts % VEC == 0;
+  if (vec_ok) {
+    const int nvc = pow2_ceil(cdiv(ncv, kWave));
+    switch (j) {
+      case 1: return launch_mla_nvc<T, WT, VEC, 1>(a, nvc);
+      case 2: return launch_mla_nvc<T, WT, VEC, 2>(a, nvc);
+      case 4: return launch_mla_nvc<T, WT, VEC, 4>(a, nvc);
+      case 8: return launch_mla_nvc<T, WT, VEC, 8>(a, nvc);
+      case 16: return launch_mla_nvc<T, WT, VEC, 16>(a, nvc);
+      default: break;
+    }
+  }
+  const int64_t grid = cdiv(a.ntok, 4);
+  hipLaunchKernelGGL((k_mla_any<T, WT>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+                     static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
+                     static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(half),
+                     static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
+                     static_cast<T*>(a.lat), a.lts, a.err);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int ember_rope(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads, void* k,
+               int64_t k_token_stride, int64_t k_head_stride, int64_t num_k_heads, int64_t head_dim,
+               const float* cos_table, const float* sin_table, int64_t table_rows, int64_t table_row_stride,
+               const int64_t* positions, int64_t num_tokens, int dtype, void* stream) {
+  using namespace ember;
+  RopeArgs a{q,        q_token_stride, q_head_stride, num_q_heads, k,        k_token_stride,
+             k_head_stride, num_k_heads, head_dim, nullptr,     nullptr,  0.f,
+             cos_table, sin_table, table_rows, table_row_stride, positions, num_tokens,
+             static_cast<hipStream_t>(stream), nullptr};
+  const int st = check_rope_args(a);
+  if (st < 0) return EMBER_OK;
+  if (st != EMBER_OK) return st;
+  if (num_tokens > 0x7fffffffLL) return EMBER_EINVAL;
+  a.err = device_error_word();
+  if (a.err == nullptr) return EMBER_ENODEV;
+  switch (dtype) {
+    case EMBER_F32: return launch_typed<float, float, false>(a);
+    case EMBER_F16: return launch_typed<_Float16, _Float16, false>(a);
+    case EMBER_BF16: return launch_typed<__bf16, __bf16, false>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
+int ember_qk_norm_rope(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads, void* k,
+                       int64_t k_token_stride, int64_t k_head_stride, int64_t num_k_heads, int64_t head_dim,
+                       const void* q_weight, const void* k_weight, int weight_dtype, float eps,
+                       const float* cos_table, const float* sin_table, int64_t table_rows,
+                       int64_t table_row_stride, const int64_t* positions, int64_t num_tokens, int dtype,
+                       void* stream) {
+  using namespace ember;
+  RopeArgs a{q,        q_token_stride, q_head_stride, num_q_heads, k,        k_token_stride,
+             k_head_stride, num_k_heads, head_dim, q_weight,    k_weight, eps,
+             cos_table, sin_table, table_rows, table_row_stride, positions, num_tokens,
+             static_cast<hipStream_t>(stream), nullptr};
+  const int st = check_rope_args(a);
+  if (st < 0) return EMBER_OK;
+  if (st != EMBER_OK) return st;
+  if (num_tokens > 0x7fffffffLL) return EMBER_EINVAL;
+  if ((num_q_heads > 0 && q_weight == nullptr) || (num_k_heads > 0 && k_weight == nullptr)) return EMBER_EINVAL;
+  if (num_k_heads == 0) a.kw = q_weight;  // never read; keeps the pointer valid
+  if (num_q_heads == 0) a.qw = k_weight;
+  if (weight_dtype != dtype && weight_dtype != EMBER_F32) return EMBER_EINVAL;
+  a.err = device_error_word();
+  if (a.err == nullptr) return EMBER_ENODEV;
+  const bool wf = weight_dtype == EMBER_F32;
+  switch (dtype) {
+    case EMBER_F32: return launch_typed<float, float, true>(a);
+    case EMBER_F16: return wf ? launch_typed<_Float16, float, true>(a) : launch_typed<_Float16, _Float16, true>(a);
+    case EMBER_BF16: return wf ? launch_typed<__bf16, float, true>(a) : launch_typed<__bf16, __bf16, true>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
+int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora_rank, const void* k_pe,
+                          int64_t k_pe_token_stride, void* q_pe, int64_t q_token_stride, int64_t q_head_stride,
+                          int64_t num_heads, int64_t rope_dim, const void* weight, int weight_dtype, float eps,
+                          const float* cos_table, const float* sin_table, int64_t table_rows,
+                          int64_t table_row_stride, const int64_t* positions, int64_t num_tokens, void* latent,
+                          int64_t latent_token_stride, int dtype, void* stream) {
+  using namespace ember;
+  if (num_tokens < 0 || kv_lora_rank <= 0 || num_heads < 0 || rope_dim <= 0 || rope_dim % 2 != 0) return EMBER_EINVAL;
+  if (kv_lora_rank > (1 << 20) || rope_dim > 4096 || num_heads > (1 << 20)) return EMBER_EINVAL;
+  if (table_rows < 0 || table_row_stride < rope_dim / 2) return EMBER_EINVAL;
+  if (weight_dtype != dtype && weight_dtype != EMBER_F32) return EMBER_EINVAL;
+  if (num_tokens == 0) return EMBER_OK;
+  if (num_tokens > 0x1ffffffffLL) return EMBER_EINVAL;
+  if (c == nullptr || k_pe == nullptr || weight == nullptr || latent == nullptr || positions == nullptr ||
+      cos_table == nullptr || sin_table == nullptr || (num_heads > 0 && q_pe == nullptr))
+    return EMBER_EINVAL;
+  if (latent_token_stride < kv_lora_rank + rope_dim) return EMBER_EINVAL;
+  MlaArgs a{c,          c_token_stride, kv_lora_rank, k_pe,      k_pe_token_stride, q_pe == nullptr ? latent : q_pe,
+            q_token_stride, q_head_stride, num_heads, rope_dim, weight,   eps,
+            cos_table,  sin_table,      table_rows,   table_row_stride, positions, num_tokens,
+            latent,     latent_token_stride, static_cast<hipStream_t>(stream), nullptr};
+  a.err = device_error_word();
+  if (a.err == nullptr) return EMBER_ENODEV;
+  const bool wf = weight_dtype == EMBER_F32 && dtype != EMBER_F32;
+  switch (dtype) {
+    case EMBER_F32: return launch_mla_typed<float, float>(a);
+    case EMBER_F16: return wf ? launch_mla_typed<_Float16, float>(a) : launch_mla_typed<_Float16, _Float16>(a);
+    case EMBER_BF16: return wf ? launch_mla_typed<__bf16, float>(a) : launch_mla_typed<__bf16, __bf16>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,74 @@
+"""nn.Module drop-ins for the callers of the fused ops.
+
+* `RMSNorm` mirrors emberserve/model/qwen2.py:30-45 (`forward`, `forward_with_residual`).
+* `Embedding` is an nn.Embedding whose forward is the gfx950 gather; it keeps `.weight`
+  [vocab, hidden] so weight tying (qwen2.py:204-205) and loading (weights.py:244) work.
+* `qwen3_pre_attention_rope` and `mla_pre_attention_rope` are the fused forms of the
+  elementwise tails of Qwen2Attention.pre_attention (qwen2.py:92-101) and
+  MLAAttention.pre_attention (deepseek.py:119-133), taking the projection output.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import ops
+from .rope import RotaryEmbedding
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden_size: int, eps: float) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.rmsnorm(x, self.weight, self.variance_epsilon)
+
+    def forward_with_residual(self, x: torch.Tensor,
+                              residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        return ops.fused_add_rmsnorm(x, residual, self.weight, self.variance_epsilon)
+
+
+class Embedding(nn.Embedding):
+    """nn.Embedding with the bit-exact gfx950 row gather as its forward on GPU weights."""
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        if self.padding_idx is None and self.max_norm is None:
+            return ops.embedding(ids, self.weight)
+        return super().forward(ids)
+
+
+def qwen3_pre_attention_rope(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
+                             q_norm: RMSNorm, k_norm: RMSNorm, rotary_emb: RotaryEmbedding,
+                             positions: torch.Tensor):
+    """`(q, k, v)` views of qkv [n, (H + 2 Hkv) * D] after Qwen3 qk-norm and rope, the
+    norm and rope done in place in one kernel (qwen2.py:92-101)."""
+    n = qkv.shape[0]
+    q_size, kv_size = num_heads * head_dim, num_kv_heads * head_dim
+    q, k, v = qkv.split([q_size, kv_size, kv_size], dim=-1)
+    q = q.view(n, num_heads, head_dim)
+    k = k.view(n, num_kv_heads, head_dim)
+    v = v.view(n, num_kv_heads, head_dim)
+    cos, sin = rotary_emb.full_tables(positions.device)
+    q, k = ops.qk_norm_rope(q, k, q_norm.weight, k_norm.weight, q_norm.variance_epsilon, cos, sin,
+                            positions)
+    return q, k, v
+
+
+def mla_pre_attention_rope(qkv_a: torch.Tensor, num_heads: int, qk_nope: int, qk_rope: int,
+                           kv_lora_rank: int, kv_a_layernorm: RMSNorm, rotary_emb: RotaryEmbedding,
+                           positions: torch.Tensor):
+    """`(q_nope, q_pe, latent)` from the fused qkv_a projection [n, H*(Dn+Dr) + R + Dr]
+    (deepseek.py:119-133 without q_lora, rope folded into the weights)."""
+    n = qkv_a.shape[0]
+    q_size = num_heads * (qk_nope + qk_rope)
+    q, ckv = qkv_a.split([q_size, kv_lora_rank + qk_rope], dim=-1)
+    q = q.view(n, num_heads, qk_nope + qk_rope)
+    q_nope, q_pe = q.split([qk_nope, qk_rope], dim=-1)
+    c, k_pe = ckv.split([kv_lora_rank, qk_rope], dim=-1)
+    cos, sin = rotary_emb.full_tables(positions.device)
+    q_pe, latent = ops.mla_latent_rope(c, k_pe, q_pe, kv_a_layernorm.weight,
+                                       kv_a_layernorm.variance_epsilon, cos, sin, positions)
+    return q_nope, q_pe, latent

@@ -1,0 +1,349 @@
+"""Fused per-layer elementwise ops on MI355X: the drop-in for emberserve/model/ops.py.
+
+The public functions keep the reference's signatures and dispatch rule
+(emberserve/model/ops.py:92-115): a GPU tensor runs the gfx950 HIP kernel of
+libember_ops.so, a CPU tensor (or any tensor with `EMBERSERVE_FUSED_OPS=0`) runs the
+PyTorch-eager form. Differences from the reference's dispatch, on purpose:
+
+* there is no silent fallback: a GPU tensor with the fused path enabled raises
+  RuntimeError when the HIP library is missing, instead of dropping to eager torch;
+* three fused entry points are added for callers that want one pass instead of several:
+  `qk_norm_rope` (qwen2.py:95-101), `mla_latent_rope` (deepseek.py:126-133) and
+  `embedding` (nn.Embedding at qwen2.py:182).
+
+The `*_hip` functions are the counterparts of the reference's `*_triton` wrappers
+(ops_triton.py:90-134): same arguments, same output allocation (torch caching allocator on
+the input's device), same in-place behaviour (rope and qk-norm rope rotate q/k in place and
+return them), launched on torch's current stream with no host synchronisation, so they can
+be recorded into a torch.cuda.graph.
+
+Numerics (vs the reference's PyTorch ops on the same inputs): the residual of
+fused_add_rmsnorm and the embedding gather are bit-exact; rope output is the same fp32
+expression as the reference (separately rounded products and sum) and is bit-exact when the
+cos/sin tables are equal; rmsnorm and silu differ only through fp32 reduction order and
+exp/rsqrt implementations, within 2 ulp of the storage dtype.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib
+from .eager import (  # noqa: F401  (re-exported: the reference's names)
+    _rotate_half,
+    embedding_torch,
+    fused_add_rmsnorm_torch,
+    mla_latent_rope_torch,
+    qk_norm_rope_torch,
+    rmsnorm_torch,
+    rope_torch,
+    silu_and_mul_torch,
+)
+
+__all__ = [
+    "fused_enabled", "rmsnorm", "fused_add_rmsnorm", "rope", "silu_and_mul", "embedding",
+    "qk_norm_rope", "mla_latent_rope", "rmsnorm_hip", "fused_add_rmsnorm_hip", "rope_hip",
+    "silu_and_mul_hip", "embedding_hip", "qk_norm_rope_hip", "mla_latent_rope_hip",
+    "rmsnorm_torch", "fused_add_rmsnorm_torch", "rope_torch", "silu_and_mul_torch",
+    "embedding_torch", "qk_norm_rope_torch", "mla_latent_rope_torch",
+]
+
+
+def fused_enabled(x: torch.Tensor) -> bool:
+    """HIP path: a GPU tensor and `EMBERSERVE_FUSED_OPS` not "0" (ops.py:43-46). Whether
+    the library is built does not enter: a missing library is an error, not a fallback."""
+    return x.is_cuda and os.environ.get("EMBERSERVE_FUSED_OPS", "1") != "0"
+
+
+def _check_indices() -> bool:
+    return os.environ.get("EMBERSERVE_CHECK_INDICES", "0") == "1"
+
+
+def _raise_index_errors() -> None:
+    flags = _lib.read_errors(clear=True)
+    if flags & _lib.ERR_EMBED_ID:
+        raise IndexError("emberserve_amd.embedding: token id out of range")
+    if flags & _lib.ERR_ROPE_POS:
+        raise IndexError("emberserve_amd.rope: position out of range of the cos/sin table")
+
+
+class _on_device:
+    """Makes `t`'s GPU current for the duration of a launch (no-op when it already is)."""
+
+    def __init__(self, t: torch.Tensor) -> None:
+        self.idx = t.device.index
+        self.prev: int | None = None
+
+    def __enter__(self) -> None:
+        cur = torch.cuda.current_device()
+        if self.idx is not None and self.idx != cur:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc) -> None:
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def _rows2d(x: torch.Tensor) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[-1] > 1 and x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def _weight_for(weight: torch.Tensor, x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """The norm weight as the kernel reads it: x's dtype, or fp32 for any other dtype (an
+    exact widening, which is what the reference's kernel does when it loads it)."""
+    if weight.device != x.device:
+        raise ValueError(f"weight on {weight.device}, activations on {x.device}")
+    w = weight if weight.dtype in (x.dtype, torch.float32) else weight.float()
+    if not w.is_contiguous():
+        w = w.contiguous()
+    return w, _lib.dtype_tag(w.dtype)
+
+
+def _tables(cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor, d: int):
+    if cos.dtype != torch.float32:
+        cos = cos.float()
+    if sin.dtype != torch.float32:
+        sin = sin.float()
+    if cos.stride(-1) != 1:
+        cos = cos.contiguous()
+    if sin.stride(-1) != 1:
+        sin = sin.contiguous()
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] < d // 2 or cos.stride(0) != sin.stride(0):
+        raise ValueError(f"cos/sin tables must both be [max_pos, >= {d // 2}] with equal strides")
+    if positions.dtype != torch.int64:
+        positions = positions.long()
+    if not positions.is_contiguous():
+        positions = positions.contiguous()
+    return cos, sin, positions
+
+
+# ---- HIP wrappers (the counterparts of ops_triton.py) ----------------------------------
+
+def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """ops_triton.py:90-97."""
+    x2 = _rows2d(x)
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    w, wtag = _weight_for(weight, x)
+    if w.numel() != x2.shape[1]:
+        raise ValueError(f"weight has {w.numel()} elements, rows have {x2.shape[1]}")
+    lib = _lib.load()
+    with _on_device(x):
+        st = lib.ember_rmsnorm(x2.data_ptr(), x2.stride(0), w.data_ptr(), wtag, out.data_ptr(),
+                               out.stride(0), x2.shape[0], x2.shape[1], float(eps),
+                               _lib.dtype_tag(x.dtype), _lib.stream_handle(x.device))
+    _lib.check(st, "ember_rmsnorm")
+    return out.view(x.shape)
+
+
+def fused_add_rmsnorm_hip(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                          eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """ops_triton.py:100-110. Returns (normed, new_residual); the inputs are not modified."""
+    if residual.dtype != x.dtype or residual.shape != x.shape:
+        raise ValueError("x and residual must share shape and dtype")
+    x2 = _rows2d(x)
+    r2 = _rows2d(residual)
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    new_res = torch.empty(r2.shape, dtype=x.dtype, device=x.device)
+    w, wtag = _weight_for(weight, x)
+    if w.numel() != x2.shape[1]:
+        raise ValueError(f"weight has {w.numel()} elements, rows have {x2.shape[1]}")
+    lib = _lib.load()
+    with _on_device(x):
+        st = lib.ember_fused_add_rmsnorm(
+            x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0), w.data_ptr(), wtag,
+            out.data_ptr(), out.stride(0), new_res.data_ptr(), new_res.stride(0), x2.shape[0],
+            x2.shape[1], float(eps), _lib.dtype_tag(x.dtype), _lib.stream_handle(x.device))
+    _lib.check(st, "ember_fused_add_rmsnorm")
+    return out.view(x.shape), new_res.view(residual.shape)
+
+
+def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+             positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """ops_triton.py:113-124: in place on q [N, H, D] and k [N, Hkv, D] (unit stride in D,
+    any other strides); returns (q, k)."""
+    n, h, d = q.shape
+    hk = k.shape[1]
+    if not (q.stride(2) == 1 and k.stride(2) == 1 and d % 2 == 0):
+        raise AssertionError("rope: q/k need unit stride in the head dim and an even head_dim")
+    if k.shape[0] != n or k.shape[2] != d or k.dtype != q.dtype:
+        raise ValueError("rope: q and k must agree in tokens, head_dim and dtype")
+    if n == 0:
+        return q, k
+    cos, sin, positions = _tables(cos, sin, positions, d)
+    lib = _lib.load()
+    with _on_device(q):
+        st = lib.ember_rope(q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
+                            k.stride(1), hk, d, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                            cos.stride(0), positions.data_ptr(), n, _lib.dtype_tag(q.dtype),
+                            _lib.stream_handle(q.device))
+    _lib.check(st, "ember_rope")
+    if _check_indices():
+        _raise_index_errors()
+    return q, k
+
+
+def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
+    """ops_triton.py:127-134."""
+    x2 = _rows2d(x)
+    inter = x2.shape[-1] // 2
+    out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)
+    if inter == 0 or x2.shape[0] == 0:
+        return out.view(*x.shape[:-1], inter)
+    lib = _lib.load()
+    with _on_device(x):
+        st = lib.ember_silu_and_mul(x2.data_ptr(), x2.stride(0), out.data_ptr(), out.stride(0),
+                                    x2.shape[0], inter, _lib.dtype_tag(x.dtype),
+                                    _lib.stream_handle(x.device))
+    _lib.check(st, "ember_silu_and_mul")
+    return out.view(*x.shape[:-1], inter)
+
+
+def embedding_hip(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """nn.Embedding forward: out[..., :] = weight[ids[...], :], bit-exact."""
+    if weight.dim() != 2:
+        raise ValueError("embedding weight must be [vocab, hidden]")
+    if ids.dtype not in (torch.int64, torch.int32):
+        raise TypeError(f"embedding ids must be int64 or int32, got {ids.dtype}")
+    flat = ids.reshape(-1)
+    if flat.dtype != torch.int64:
+        flat = flat.long()
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    w = weight if weight.stride(1) == 1 else weight.contiguous()
+    out = torch.empty((flat.shape[0], w.shape[1]), dtype=w.dtype, device=w.device)
+    if flat.shape[0] == 0:
+        return out.view(*ids.shape, w.shape[1])
+    lib = _lib.load()
+    with _on_device(w):
+        st = lib.ember_embedding(flat.data_ptr(), flat.shape[0], w.data_ptr(), w.shape[0], w.shape[1],
+                                 w.stride(0), out.data_ptr(), out.stride(0), w.element_size(),
+                                 _lib.stream_handle(w.device))
+    _lib.check(st, "ember_embedding")
+    if _check_indices():
+        _raise_index_errors()
+    return out.view(*ids.shape, w.shape[1])
+
+
+def qk_norm_rope_hip(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                     k_weight: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                     positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Qwen3 per-head RMSNorm of q and k, then neox rope, in place on the q/k views
+    (qwen2.py:95-101 in one kernel); returns (q, k)."""
+    n, h, d = q.shape
+    hk = k.shape[1]
+    if not (q.stride(2) == 1 and k.stride(2) == 1 and d % 2 == 0):
+        raise AssertionError("qk_norm_rope: q/k need unit stride in the head dim and an even head_dim")
+    if k.shape[0] != n or k.shape[2] != d or k.dtype != q.dtype:
+        raise ValueError("qk_norm_rope: q and k must agree in tokens, head_dim and dtype")
+    if q_weight.numel() != d or k_weight.numel() != d:
+        raise ValueError("qk_norm_rope: q/k norm weights must have head_dim elements")
+    if n == 0:
+        return q, k
+    qw, qtag = _weight_for(q_weight, q)
+    kw, ktag = _weight_for(k_weight, q)
+    if qtag != ktag:
+        qw, kw, qtag = qw.float(), kw.float(), _lib.F32
+    cos, sin, positions = _tables(cos, sin, positions, d)
+    lib = _lib.load()
+    with _on_device(q):
+        st = lib.ember_qk_norm_rope(q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
+                                    k.stride(1), hk, d, qw.data_ptr(), kw.data_ptr(), qtag, float(eps),
+                                    cos.data_ptr(), sin.data_ptr(), cos.shape[0], cos.stride(0),
+                                    positions.data_ptr(), n, _lib.dtype_tag(q.dtype),
+                                    _lib.stream_handle(q.device))
+    _lib.check(st, "ember_qk_norm_rope")
+    if _check_indices():
+        _raise_index_errors()
+    return q, k
+
+
+def mla_latent_rope_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor,
+                        weight: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                        positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """MLA latent path (deepseek.py:126-133, rope folded into the weights): rmsnorm of the
+    latent c [N, R], rope of the single key head k_pe [N, Dr] (or [N, 1, Dr]) into a new
+    latent [N, R + Dr], and rope of q_pe [N, H, Dr] in place. c and k_pe are not modified.
+    Returns (q_pe, latent)."""
+    n, r = c.shape
+    kp = k_pe.reshape(k_pe.shape[0], -1)
+    nh, dr = q_pe.shape[1], q_pe.shape[2]
+    if kp.shape != (n, dr) or q_pe.shape[0] != n:
+        raise ValueError("mla_latent_rope: c [N, R], k_pe [N, Dr], q_pe [N, H, Dr] expected")
+    if c.stride(1) != 1 or kp.stride(1) != 1 or q_pe.stride(2) != 1 or dr % 2 != 0:
+        raise AssertionError("mla_latent_rope: unit innermost stride and an even rope dim required")
+    if c.dtype != kp.dtype or c.dtype != q_pe.dtype:
+        raise ValueError("mla_latent_rope: c, k_pe and q_pe must share a dtype")
+    if weight.numel() != r:
+        raise ValueError("mla_latent_rope: weight must have kv_lora_rank elements")
+    latent = torch.empty((n, r + dr), dtype=c.dtype, device=c.device)
+    if n == 0:
+        return q_pe, latent
+    w, wtag = _weight_for(weight, c)
+    cos, sin, positions = _tables(cos, sin, positions, dr)
+    lib = _lib.load()
+    with _on_device(c):
+        st = lib.ember_mla_latent_rope(
+            c.data_ptr(), c.stride(0), r, kp.data_ptr(), kp.stride(0), q_pe.data_ptr(), q_pe.stride(0),
+            q_pe.stride(1), nh, dr, w.data_ptr(), wtag, float(eps), cos.data_ptr(), sin.data_ptr(),
+            cos.shape[0], cos.stride(0), positions.data_ptr(), n, latent.data_ptr(), latent.stride(0),
+            _lib.dtype_tag(c.dtype), _lib.stream_handle(c.device))
+    _lib.check(st, "ember_mla_latent_rope")
+    if _check_indices():
+        _raise_index_errors()
+    return q_pe, latent
+
+
+# ---- dispatch (ops.py:92-115 plus the fused additions) ----------------------------------
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    if fused_enabled(x):
+        return rmsnorm_hip(x, weight, eps)
+    return rmsnorm_torch(x, weight, eps)
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    if fused_enabled(x):
+        return fused_add_rmsnorm_hip(x, residual, weight, eps)
+    return fused_add_rmsnorm_torch(x, residual, weight, eps)
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    if fused_enabled(q):
+        return rope_hip(q, k, cos, sin, positions)
+    return rope_torch(q, k, cos, sin, positions)
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    if fused_enabled(x):
+        return silu_and_mul_hip(x)
+    return silu_and_mul_torch(x)
+
+
+def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    if fused_enabled(weight):
+        return embedding_hip(ids, weight)
+    return embedding_torch(ids, weight)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                 eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                 positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    if fused_enabled(q):
+        return qk_norm_rope_hip(q, k, q_weight, k_weight, eps, cos, sin, positions)
+    return qk_norm_rope_torch(q, k, q_weight, k_weight, eps, cos, sin, positions)
+
+
+def mla_latent_rope(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, weight: torch.Tensor,
+                    eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                    positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    if fused_enabled(c):
+        return mla_latent_rope_hip(c, k_pe, q_pe, weight, eps, cos, sin, positions)
+    return mla_latent_rope_torch(c, k_pe, q_pe, weight, eps, cos, sin, positions)

@@ -1,0 +1,158 @@
+/*
+ * ember_ops.h - C ABI of libember_ops.so, the gfx950 (MI355X) kernels behind emberserve's
+ * fused per-layer elementwise ops.
+ *
+ * Every entry point takes raw device pointers, element counts and element strides
+ * (int64), a dtype tag and an opaque stream handle (a hipStream_t, passed as void*; NULL
+ * is the null stream). Nothing is allocated, nothing synchronises the host, and every
+ * launch goes on the given stream, so all entry points are safe under stream/graph
+ * capture. Strides are in elements of the tensor's own dtype; the innermost dimension is
+ * always unit-stride.
+ *
+ * Return value: EMBER_OK (0) or one of the EMBER_E* codes below. Argument errors are
+ * detected on the host before any launch; a failed launch returns EMBER_ELAUNCH.
+ * ember_status_string() names a code.
+ *
+ * Index safety: positions and token ids are checked on the device. An out-of-range
+ * position leaves that token's rows untouched, an out-of-range id writes a zero row; both
+ * set a bit in a per-device error word that ember_read_errors() returns (and optionally
+ * clears). Reading it synchronises, so callers read it only in debug paths.
+ *
+ * Reference interfaces replaced (paths relative to the emberserve repository):
+ *   ember_rmsnorm             emberserve/model/ops.py:92-95  (rmsnorm) and
+ *                             emberserve/model/ops_triton.py:90-97 (rmsnorm_triton)
+ *   ember_fused_add_rmsnorm   emberserve/model/ops.py:98-102 (fused_add_rmsnorm) and
+ *                             emberserve/model/ops_triton.py:100-110
+ *   ember_rope                emberserve/model/ops.py:105-109 (rope) and
+ *                             emberserve/model/ops_triton.py:113-124 (rope_triton)
+ *   ember_silu_and_mul        emberserve/model/ops.py:112-115 (silu_and_mul) and
+ *                             emberserve/model/ops_triton.py:127-134
+ *   ember_embedding           torch.nn.Embedding.forward as used by
+ *                             emberserve/model/qwen2.py:172,182 and deepseek.py:197,205
+ *   ember_qk_norm_rope        the q_norm/k_norm + rotary_emb sequence of
+ *                             emberserve/model/qwen2.py:95-101 (two rmsnorm + one rope)
+ *   ember_mla_latent_rope     the kv_a_layernorm + rotary_emb + cat sequence of
+ *                             emberserve/model/deepseek.py:124-133
+ */
+#ifndef EMBER_OPS_H
+#define EMBER_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags (activations and, where stated, weights) */
+#define EMBER_F32 0
+#define EMBER_F16 1
+#define EMBER_BF16 2
+
+/* status codes */
+#define EMBER_OK 0
+#define EMBER_EINVAL 1      /* bad shape, stride, dtype or pointer */
+#define EMBER_EALIGN 2      /* reserved: misalignment is handled by scalar kernels */
+#define EMBER_ELAUNCH 3     /* the HIP launch itself failed */
+#define EMBER_ENODEV 4      /* no HIP device / runtime call failed */
+
+/* bits of the device error word */
+#define EMBER_ERR_EMBED_ID 1u   /* a token id outside [0, vocab) */
+#define EMBER_ERR_ROPE_POS 2u   /* a position outside [0, table_rows) */
+
+/* ABI version, bumped on any signature change. */
+int ember_abi_version(void);
+
+/* Static description of a status code. */
+const char* ember_status_string(int status);
+
+/* Copies the current device's error word into *flags (if non-NULL) and, when clear != 0,
+ * zeroes it. Synchronises the device. Returns EMBER_OK or EMBER_ENODEV. */
+int ember_read_errors(uint32_t* flags, int clear);
+
+/* RMSNorm of `rows` rows of `cols` elements:
+ *   out = round(w * round(x * rsqrt(mean(x^2) + eps)))
+ * fp32 math, rounding to `dtype` at the two points the reference rounds.
+ * `weight` is [cols], contiguous, of dtype `weight_dtype` (== dtype, or EMBER_F32).
+ * Replaces ops.py:92-95 / ops_triton.py:90-97 (_rmsnorm_kernel with HAS_RESIDUAL=0). */
+int ember_rmsnorm(const void* x, int64_t x_row_stride,
+                  const void* weight, int weight_dtype,
+                  void* out, int64_t out_row_stride,
+                  int64_t rows, int64_t cols, float eps, int dtype, void* stream);
+
+/* Fused residual add + RMSNorm:
+ *   residual_out = round(residual + x);  out = rmsnorm(residual_out)
+ * Inputs are not modified (outputs may not alias them).
+ * Replaces ops.py:98-102 / ops_triton.py:100-110 (_rmsnorm_kernel with HAS_RESIDUAL=1). */
+int ember_fused_add_rmsnorm(const void* x, int64_t x_row_stride,
+                            const void* residual, int64_t residual_row_stride,
+                            const void* weight, int weight_dtype,
+                            void* out, int64_t out_row_stride,
+                            void* residual_out, int64_t residual_out_row_stride,
+                            int64_t rows, int64_t cols, float eps, int dtype, void* stream);
+
+/* Neox (rotate-half) rotary embedding, in place on q [tokens, num_q_heads, head_dim] and
+ * k [tokens, num_k_heads, head_dim]:
+ *   o[i]      = round(x[i] * c[i] - x[i + D/2] * s[i])
+ *   o[i+D/2]  = round(x[i+D/2] * c[i] + x[i] * s[i])      for i < D/2
+ * with c, s = cos/sin[positions[t]][i], fp32 tables of `table_rows` rows, row stride
+ * `table_row_stride` floats, whose two halves are equal (RotaryEmbedding builds
+ * cat(freqs, freqs)). Each product and the sum are rounded separately in fp32 (no FMA),
+ * as the reference's element-wise tensor ops are. num_k_heads may be 0 (k unused).
+ * Replaces ops.py:105-109 / ops_triton.py:113-124 (_rope_kernel). */
+int ember_rope(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads,
+               void* k, int64_t k_token_stride, int64_t k_head_stride, int64_t num_k_heads,
+               int64_t head_dim,
+               const float* cos_table, const float* sin_table,
+               int64_t table_rows, int64_t table_row_stride,
+               const int64_t* positions, int64_t num_tokens, int dtype, void* stream);
+
+/* SwiGLU activation: out[r, j] = round(round(silu(x[r, j])) * x[r, inter + j]).
+ * x is [rows, 2*inter] (row stride x_row_stride), out is [rows, inter].
+ * Replaces ops.py:112-115 / ops_triton.py:127-134 (_silu_and_mul_kernel). */
+int ember_silu_and_mul(const void* x, int64_t x_row_stride,
+                       void* out, int64_t out_row_stride,
+                       int64_t rows, int64_t inter, int dtype, void* stream);
+
+/* Row gather: out[t, :] = weight[ids[t], :], a bit-exact copy of `hidden` elements of
+ * `elem_bytes` bytes each (1, 2, 4 or 8). ids outside [0, vocab) give a zero row and set
+ * EMBER_ERR_EMBED_ID. Replaces torch.nn.Embedding.forward (F.embedding) as called at
+ * qwen2.py:182 / deepseek.py:205 / attn/piecewise_graphs.py:176. */
+int ember_embedding(const int64_t* ids, int64_t num_tokens,
+                    const void* weight, int64_t vocab, int64_t hidden, int64_t weight_row_stride,
+                    void* out, int64_t out_row_stride, int64_t elem_bytes, void* stream);
+
+/* Qwen3 per-head QK-RMSNorm fused with neox rope, in place on q and k (same layout rules
+ * as ember_rope). Per head row: y = round(w * round(x * rsqrt(mean(x^2) + eps))), then
+ * the rope of ember_rope applied to y. q_weight, k_weight are [head_dim] of weight_dtype.
+ * Same result as rmsnorm on [tokens*heads, head_dim] followed by rope
+ * (qwen2.py:95-101), in one pass over q and k. */
+int ember_qk_norm_rope(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads,
+                       void* k, int64_t k_token_stride, int64_t k_head_stride, int64_t num_k_heads,
+                       int64_t head_dim,
+                       const void* q_weight, const void* k_weight, int weight_dtype, float eps,
+                       const float* cos_table, const float* sin_table,
+                       int64_t table_rows, int64_t table_row_stride,
+                       const int64_t* positions, int64_t num_tokens, int dtype, void* stream);
+
+/* MLA latent path (deepseek.py:124-133 with the rope permutation folded into the
+ * weights):
+ *   latent[t, :R]      = rmsnorm(c[t, :R], weight, eps)            (R = kv_lora_rank)
+ *   latent[t, R:R+Dr]  = rope(k_pe[t, :Dr])                         (one key head)
+ *   q_pe[t, h, :Dr]    = rope(q_pe[t, h, :Dr])  in place, h < num_heads
+ * c and k_pe are read only. q_pe is typically the rope slice of q [T, H, Dn+Dr] (head
+ * stride Dn+Dr). Rope as in ember_rope, Dr = rope_dim. */
+int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora_rank,
+                          const void* k_pe, int64_t k_pe_token_stride,
+                          void* q_pe, int64_t q_token_stride, int64_t q_head_stride, int64_t num_heads,
+                          int64_t rope_dim,
+                          const void* weight, int weight_dtype, float eps,
+                          const float* cos_table, const float* sin_table,
+                          int64_t table_rows, int64_t table_row_stride,
+                          const int64_t* positions, int64_t num_tokens,
+                          void* latent, int64_t latent_token_stride, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMBER_OPS_H */

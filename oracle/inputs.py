@@ -1,0 +1,72 @@
+"""Seeded synthetic inputs for the five BASELINE configurations (TEST INFRASTRUCTURE ONLY:
+shared by the parity tests, smoke() and bench.py so all of them draw identical tensors).
+
+Draws follow the configuration text: activations N(0, 1) (silu input N(0, 2), i.e. std 2),
+norm weights N(1, 0.1), the embedding table N(0, 0.02), positions and ids uniform. All
+draws come from a CPU torch.Generator, so they do not depend on the device.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def normal(shape, dtype, seed, mean=0.0, std=1.0) -> torch.Tensor:
+    return (torch.randn(*shape, generator=gen(seed)) * std + mean).to(dtype)
+
+
+def uniform_ints(n: int, high: int, seed: int) -> torch.Tensor:
+    return torch.randint(0, high, (n,), generator=gen(seed), dtype=torch.int64)
+
+
+def add_rmsnorm_inputs(tokens: int, hidden: int, dtype, seed: int = 0):
+    """Configs 1 and 4c: x, residual N(0,1); weight N(1, 0.1)."""
+    x = normal((tokens, hidden), dtype, seed)
+    r = normal((tokens, hidden), dtype, seed + 1)
+    w = normal((hidden,), dtype, seed + 2, mean=1.0, std=0.1)
+    return x, r, w
+
+
+def rope_inputs(tokens: int, hq: int, hk: int, d: int, max_pos: int, dtype, seed: int = 0):
+    """Config 2: q [T, Hq, D], k [T, Hk, D] N(0,1); positions uniform in [0, max_pos)."""
+    q = normal((tokens, hq, d), dtype, seed)
+    k = normal((tokens, hk, d), dtype, seed + 1)
+    pos = uniform_ints(tokens, max_pos, seed + 2)
+    return q, k, pos
+
+
+def silu_inputs(tokens: int, inter: int, dtype, seed: int = 0):
+    """Config 3: fused gate/up [T, 2I] drawn N(0, 2) (std 2)."""
+    return normal((tokens, 2 * inter), dtype, seed, std=2.0)
+
+
+def embedding_inputs(tokens: int, vocab: int, hidden: int, dtype, seed: int = 0):
+    """Config 4a: table N(0, 0.02), ids uniform over the vocabulary."""
+    w = normal((vocab, hidden), dtype, seed, std=0.02)
+    ids = uniform_ints(tokens, vocab, seed + 1)
+    return ids, w
+
+
+def qkv_inputs(tokens: int, hq: int, hk: int, d: int, max_pos: int, dtype, seed: int = 0):
+    """Config 4b: the fused qkv projection output [T, (Hq + 2 Hk) * D] N(0,1), per-head
+    norm weights N(1, 0.1), positions uniform."""
+    qkv = normal((tokens, (hq + 2 * hk) * d), dtype, seed)
+    qw = normal((d,), dtype, seed + 1, mean=1.0, std=0.1)
+    kw = normal((d,), dtype, seed + 2, mean=1.0, std=0.1)
+    pos = uniform_ints(tokens, max_pos, seed + 3)
+    return qkv, qw, kw, pos
+
+
+def mla_inputs(tokens: int, heads: int, nope: int, rope_dim: int, rank: int, max_pos: int, dtype,
+               seed: int = 0):
+    """Config 5: kv_a [T, R + Dr] and q [T, H, Dn + Dr] N(0,1), weight N(1, 0.1),
+    positions uniform."""
+    kv_a = normal((tokens, rank + rope_dim), dtype, seed)
+    q = normal((tokens, heads, nope + rope_dim), dtype, seed + 1)
+    w = normal((rank,), dtype, seed + 2, mean=1.0, std=0.1)
+    pos = uniform_ints(tokens, max_pos, seed + 3)
+    return kv_a, q, w, pos

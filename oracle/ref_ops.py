@@ -1,0 +1,131 @@
+"""CPU restatement of the reference's PyTorch-eager ops (TEST INFRASTRUCTURE ONLY).
+
+Each function restates, op for op and in the same dtypes, the reference function named in
+its docstring, so its rounding structure is the reference's by construction: it runs the
+same PyTorch CPU kernels (torch 2.10 here; the reference pins torch>=2.2,
+pyproject.toml:14). The reference defines these ops as "whatever torch-eager computes", so
+torch CPU *is* the arithmetic being restated.
+
+How each function is pinned (tests/test_oracle.py), beyond this restatement:
+  rmsnorm, fused_add_rmsnorm   float64 closed form within 1 ulp of the storage dtype; a
+                               constant row's closed form; exact invariance under
+                               power-of-two scaling (eps = 0); the residual equals numpy's
+                               IEEE float16 sum bit for bit (bf16: explicit RNE in numpy);
+                               the reference's own test cases (shapes, seeds).
+  rope, rope_tables            float64 complex-number rotation (the reference's own
+                               closed-form test, tests/test_rope.py:17-27); identity at
+                               position 0; norm preservation; relative-position invariance;
+                               rotate_half on arange(6) (test_rope.py:31-32); the tables
+                               against float64 cos/sin; Llama-3 scaling bands.
+  silu_and_mul                 float64 g*sigmoid(g)*u within 2 ulp; silu(0) = 0.
+  embedding                    numpy.take, bit-exact.
+  qk_norm_rope, mla_latent_rope  float64 normalise-then-rotate closed forms; untouched
+                               columns bit-exact.
+No function is left unpinned.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """emberserve/model/ops.py:51-55 (rmsnorm_torch)."""
+    xf = x.float()
+    variance = xf.pow(2).mean(-1, keepdim=True)
+    xf = xf * torch.rsqrt(variance + eps)
+    return weight * xf.to(x.dtype)
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """emberserve/model/ops.py:58-63 (fused_add_rmsnorm_torch): (normed, new_residual)."""
+    residual = residual + x
+    return rmsnorm(residual, weight, eps), residual
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """emberserve/model/ops.py:66-68 (_rotate_half)."""
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """emberserve/model/ops.py:71-81 (rope_torch): new tensors."""
+    c = cos[positions][:, None, :]
+    s = sin[positions][:, None, :]
+
+    def rot(x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        return (xf * c + rotate_half(xf) * s).to(x.dtype)
+
+    return rot(q), rot(k)
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """emberserve/model/ops.py:84-87 (silu_and_mul_torch)."""
+    inter = x.shape[-1] // 2
+    return F.silu(x[..., :inter]) * x[..., inter:]
+
+
+def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """torch.nn.Embedding.forward as used at emberserve/model/qwen2.py:182."""
+    return F.embedding(ids, weight)
+
+
+def llama3_scale_inv_freq(inv_freq: torch.Tensor, scaling: dict) -> torch.Tensor:
+    """emberserve/model/rope.py:36-51."""
+    factor = float(scaling["factor"])
+    low_freq_factor = float(scaling["low_freq_factor"])
+    high_freq_factor = float(scaling["high_freq_factor"])
+    old_context_len = float(scaling["original_max_position_embeddings"])
+    low_freq_wavelen = old_context_len / low_freq_factor
+    high_freq_wavelen = old_context_len / high_freq_factor
+    wavelen = 2 * math.pi / inv_freq
+    inv_freq_llama = torch.where(wavelen > low_freq_wavelen, inv_freq / factor, inv_freq)
+    smooth = (old_context_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    smoothed = (1 - smooth) * inv_freq_llama / factor + smooth * inv_freq_llama
+    is_medium = ~(wavelen < high_freq_wavelen) & ~(wavelen > low_freq_wavelen)
+    return torch.where(is_medium, smoothed, inv_freq_llama)
+
+
+def rope_tables(head_dim: int, max_position_embeddings: int, base: float,
+                rope_scaling: dict | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """emberserve/model/rope.py:68-82 (inv_freq + _build_tables), on the CPU: fp32
+    cos/sin [max_pos, head_dim] with equal halves."""
+    exponent = torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim
+    inv = 1.0 / (float(base) ** exponent)
+    if rope_scaling and rope_scaling.get("rope_type", rope_scaling.get("type")) == "llama3":
+        inv = llama3_scale_inv_freq(inv, rope_scaling)
+    positions = torch.arange(max_position_embeddings, dtype=torch.float32)
+    freqs = torch.outer(positions, inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                 eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                 positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """emberserve/model/qwen2.py:95-101: q_norm/k_norm on [n*heads, head_dim] rows (the
+    reshape copies the split views), view back, then rotary_emb -> ops.rope."""
+    n, h, d = q.shape
+    hk = k.shape[1]
+    qn = rmsnorm(q.reshape(n * h, d), q_weight, eps).view(n, h, d)
+    kn = rmsnorm(k.reshape(n * hk, d), k_weight, eps).view(n, hk, d)
+    return rope(qn, kn, cos, sin, positions)
+
+
+def mla_latent_rope(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, weight: torch.Tensor,
+                    eps: float, cos: torch.Tensor, sin: torch.Tensor,
+                    positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """emberserve/model/deepseek.py:126-133 (rope_folded branch): c = kv_a_layernorm(c);
+    q_pe, k_pe = rotary_emb(q_pe, k_pe.unsqueeze(1)); latent = cat([c, k_pe.squeeze(1)]).
+    Returns (q_pe, latent)."""
+    c = rmsnorm(c, weight, eps)
+    q_pe, k_pe = rope(q_pe, k_pe.reshape(k_pe.shape[0], -1).unsqueeze(1), cos, sin, positions)
+    latent = torch.cat([c, k_pe.squeeze(1)], dim=-1)
+    return q_pe, latent

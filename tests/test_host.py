@@ -1,0 +1,144 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every entry
+point include/ember_ops.h declares, argument validation rejects bad calls before any
+launch, the Python drop-in keeps the reference's API, and CPU tensors take the eager path
+exactly as the reference's dispatch does (emberserve/model/ops.py:43-46, 92-115)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from emberserve_amd import _lib, layers, ops, rope
+from oracle import ref_ops as ref
+from tests.helpers import assert_bitexact
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ember_ops.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(ember_\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ["ember_rmsnorm", "ember_fused_add_rmsnorm", "ember_rope", "ember_silu_and_mul",
+              "ember_embedding", "ember_qk_norm_rope", "ember_mla_latent_rope"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.ember_abi_version() == _lib.ABI_VERSION
+    assert lib.ember_status_string(0) == b"ok"
+    assert b"invalid" in lib.ember_status_string(1)
+    assert lib.ember_status_string(99) == b"unknown status"
+
+
+def test_argument_validation_happens_before_any_launch():
+    """Bad shapes and dtypes return EMBER_EINVAL (1) without touching HIP, so these run
+    without a GPU; a zero-row call is a successful no-op."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: the calls are rejected first
+    assert lib.ember_rmsnorm(p, 64, p, 1, p, 64, -1, 64, 1e-6, 1, None) == 1  # rows < 0
+    assert lib.ember_rmsnorm(p, 64, p, 1, p, 64, 4, 0, 1e-6, 1, None) == 1  # cols == 0
+    assert lib.ember_rmsnorm(p, 64, p, 2, p, 64, 4, 64, 1e-6, 1, None) == 1  # bf16 weight, fp16 x
+    assert lib.ember_rmsnorm(p, 64, p, 7, p, 64, 4, 64, 1e-6, 7, None) == 1  # dtype tag
+    assert lib.ember_rmsnorm(p, 64, p, 1, p, 64, 0, 64, 1e-6, 1, None) == 0  # nothing to do
+    assert lib.ember_fused_add_rmsnorm(p, 64, None, 64, p, 1, p, 64, p, 64, 4, 64, 1e-6, 1, None) == 1
+    assert lib.ember_silu_and_mul(p, 10, p, 5, 4, 8, 1, None) == 1  # row stride < 2*inter
+    assert lib.ember_silu_and_mul(p, 16, p, 8, 0, 8, 1, None) == 0
+    assert lib.ember_embedding(p, 4, p, 10, 64, 64, p, 64, 3, None) == 1  # elem_bytes 3
+    assert lib.ember_embedding(p, 0, p, 10, 64, 64, p, 64, 2, None) == 0
+    assert lib.ember_rope(p, 64, 64, 1, p, 64, 64, 1, 63, p, p, 8, 64, p, 4, 2, None) == 1  # odd D
+    assert lib.ember_rope(p, 64, 64, 1, p, 64, 64, 1, 64, p, p, 8, 16, p, 4, 2, None) == 1  # table too narrow
+    assert lib.ember_rope(p, 64, 64, 1, p, 64, 64, 1, 64, p, p, 8, 64, p, 0, 2, None) == 0
+    assert lib.ember_mla_latent_rope(p, 576, 512, p, 576, p, 192, 192, 16, 64, p, 2, 1e-6, p, p, 8, 64,
+                                     p, 4, p, 500, 2, None) == 1  # latent row too short
+
+
+def test_ops_api_mirrors_the_reference():
+    for name in ["fused_enabled", "rmsnorm", "fused_add_rmsnorm", "rope", "silu_and_mul",
+                 "rmsnorm_torch", "fused_add_rmsnorm_torch", "rope_torch", "silu_and_mul_torch",
+                 "qk_norm_rope", "mla_latent_rope", "embedding"]:
+        assert callable(getattr(ops, name)), name
+    assert callable(rope.RotaryEmbedding) and callable(rope.rotate_half)
+
+
+def test_dispatch_uses_torch_off_gpu():
+    """ops.py:100-104 of the reference's test: CPU tensors stay on the eager path."""
+    x = torch.randn(2, 64)
+    w = torch.ones(64)
+    assert not ops.fused_enabled(x)
+    torch.testing.assert_close(ops.rmsnorm(x, w, 1e-6), ops.rmsnorm_torch(x, w, 1e-6))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_eager_path_equals_the_oracle(dtype):
+    """The package's eager forms (CPU tensors) give the oracle's bits."""
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(5, 128, generator=g) * 2).to(dtype)
+    r = torch.randn(5, 128, generator=g).to(dtype)
+    w = (torch.randn(128, generator=g) * 0.1 + 1).to(dtype)
+    assert_bitexact(ops.rmsnorm(x, w, 1e-6), ref.rmsnorm(x, w, 1e-6))
+    a, b = ops.fused_add_rmsnorm(x, r, w, 1e-6)
+    c, d = ref.fused_add_rmsnorm(x, r, w, 1e-6)
+    assert_bitexact(a, c)
+    assert_bitexact(b, d)
+    assert_bitexact(ops.silu_and_mul(x), ref.silu_and_mul(x))
+    cos, sin = ref.rope_tables(64, 32, 1e4)
+    q = x.view(5, 2, 64)
+    pos = torch.tensor([0, 3, 31, 7, 1])
+    for got, want in zip(ops.rope(q, q[:, :1], cos, sin, pos), ref.rope(q, q[:, :1], cos, sin, pos)):
+        assert_bitexact(got, want)
+    ids = torch.tensor([3, 1, 4])
+    assert_bitexact(ops.embedding(ids, x), ref.embedding(ids, x))
+    for got, want in zip(ops.qk_norm_rope(q, q[:, :1], w[:64], w[64:], 1e-6, cos, sin, pos),
+                         ref.qk_norm_rope(q, q[:, :1], w[:64], w[64:], 1e-6, cos, sin, pos)):
+        assert_bitexact(got, want)
+
+
+def test_rotary_module_tables_match_oracle_and_forward_on_cpu():
+    mod = rope.RotaryEmbedding(64, 256, 1e6)
+    pos = torch.tensor([0, 5, 255])
+    cos, sin = mod.tables(pos)
+    rc, rs = ref.rope_tables(64, 256, 1e6)
+    assert_bitexact(cos, rc[pos])
+    assert_bitexact(sin, rs[pos])
+    q = torch.randn(3, 2, 64)
+    qo, _ = mod(q, q[:, :1], pos)
+    assert_bitexact(qo, ref.rope(q, q[:, :1], rc, rs, pos)[0])
+
+
+def test_layers_on_cpu():
+    norm = layers.RMSNorm(64, 1e-6)
+    x = torch.randn(3, 64)
+    assert_bitexact(norm(x), ref.rmsnorm(x, norm.weight.detach(), 1e-6))
+    emb = layers.Embedding(10, 8)
+    ids = torch.tensor([1, 9])
+    assert_bitexact(emb(ids).detach(), emb.weight.detach()[ids])
+    # Qwen3 pre-attention tail on a fused qkv buffer
+    n, hq, hk, d = 4, 4, 2, 64
+    qkv = torch.randn(n, (hq + 2 * hk) * d)
+    qn, kn = layers.RMSNorm(d, 1e-6), layers.RMSNorm(d, 1e-6)
+    rot = rope.RotaryEmbedding(d, 64, 1e6)
+    pos = torch.tensor([0, 1, 2, 63])
+    q, k, v = layers.qwen3_pre_attention_rope(qkv, hq, hk, d, qn, kn, rot, pos)
+    cos, sin = ref.rope_tables(d, 64, 1e6)
+    wq, wk = ref.qk_norm_rope(qkv[:, :hq * d].view(n, hq, d), qkv[:, hq * d:(hq + hk) * d].view(n, hk, d),
+                              qn.weight.detach(), kn.weight.detach(), 1e-6, cos, sin, pos)
+    assert_bitexact(q.detach(), wq)
+    assert_bitexact(k.detach(), wk)
+    assert_bitexact(v, qkv[:, (hq + hk) * d:].view(n, hk, d))

@@ -1,0 +1,285 @@
+"""Pins the CPU oracle (oracle/ref_ops.py) against what the mathematics fixes, so that the
+GPU parity tests compare against something checked: float64 closed forms, exact
+invariances, IEEE sums done by numpy, and the reference's own closed-form rope tests
+(tests/test_rope.py of the reference). Each check is chosen so that a plausible slip in the
+restatement (a dropped eps, a wrong half in rotate_half, a swapped sign, rounding at the
+wrong point) fails it.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import inputs as gen
+from oracle import ref_ops as ref
+from tests.helpers import assert_bitexact, assert_ulp, ulp_diff
+
+torch.set_num_threads(4)
+
+
+def _rand(*shape, dtype, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _round_bf16_np(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even of float32 values to bfloat16, returned as float32 (numpy has
+    no bfloat16: done on the bit pattern)."""
+    b = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (b + 0x7FFF + ((b >> 16) & 1)) >> 16 << 16
+    return rounded.astype(np.uint32).view(np.float32)
+
+
+# ---------------------------------------------------------------- rmsnorm
+
+def _rmsnorm_f64(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xd = x.double()
+    inv = 1.0 / torch.sqrt((xd * xd).mean(-1, keepdim=True) + eps)
+    y = (xd * inv).to(x.dtype).double()  # the reference rounds before the weight multiply
+    return (y * w.double()).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hidden", [64, 896, 4096])
+def test_rmsnorm_matches_float64(dtype, hidden):
+    x = _rand(9, hidden, dtype=dtype, seed=1, scale=3.0)
+    w = _rand(hidden, dtype=dtype, seed=2, scale=0.5) + 1.0
+    got = ref.rmsnorm(x, w, 1e-6)
+    want = _rmsnorm_f64(x, w, 1e-6)
+    # the inner rounding happens at the same point on both sides; only fp32 vs fp64
+    # arithmetic separates them
+    assert_ulp(got, want, 1 if dtype != torch.float32 else 4, "rmsnorm vs float64")
+
+
+def test_rmsnorm_eps_enters():
+    """A dropped or misplaced eps shows on a row of tiny values: eps dominates there."""
+    x = torch.full((1, 16), 1e-4, dtype=torch.float32)
+    w = torch.ones(16)
+    got = ref.rmsnorm(x, w, 1e-6)
+    want = 1e-4 / math.sqrt(1e-8 + 1e-6)
+    torch.testing.assert_close(got, torch.full((1, 16), want), atol=0, rtol=1e-6)
+
+
+def test_rmsnorm_constant_row_closed_form():
+    for v in [0.5, -3.0, 7.25]:
+        x = torch.full((2, 128), v, dtype=torch.float32)
+        w = torch.linspace(0.5, 1.5, 128)
+        got = ref.rmsnorm(x, w, 1e-6)
+        want = w * (v / math.sqrt(v * v + 1e-6))
+        torch.testing.assert_close(got, want.expand(2, 128), atol=0, rtol=2e-7)
+
+
+def test_rmsnorm_power_of_two_scale_invariance():
+    """With eps = 0, scaling a row by 2^k leaves the output bit-identical (every step is
+    exact under power-of-two scaling)."""
+    x = _rand(6, 896, dtype=torch.float16, seed=3)
+    w = _rand(896, dtype=torch.float16, seed=4, scale=0.2) + 1.0
+    assert_bitexact(ref.rmsnorm(x * 4, w, 0.0), ref.rmsnorm(x, w, 0.0), "x4")
+    assert_bitexact(ref.rmsnorm(x / 8, w, 0.0), ref.rmsnorm(x, w, 0.0), "/8")
+
+
+def test_rmsnorm_unit_rms():
+    x = _rand(16, 4096, dtype=torch.float32, seed=5, scale=5.0)
+    out = ref.rmsnorm(x, torch.ones(4096), 1e-6)
+    rms = out.pow(2).mean(-1).sqrt()
+    torch.testing.assert_close(rms, torch.ones(16), atol=1e-5, rtol=0)
+
+
+# ---------------------------------------------------------------- fused add
+
+def test_fused_add_residual_is_the_ieee_fp16_sum():
+    x = _rand(7, 896, dtype=torch.float16, seed=3)
+    r = _rand(7, 896, dtype=torch.float16, seed=4, scale=4.0)
+    w = _rand(896, dtype=torch.float16, seed=5, scale=0.3) + 1.0
+    normed, res = ref.fused_add_rmsnorm(x, r, w, 1e-6)
+    want = (r.numpy() + x.numpy()).astype(np.float16)
+    assert np.array_equal(res.numpy().view(np.uint16), want.view(np.uint16))
+    assert_bitexact(normed, ref.rmsnorm(res, w, 1e-6), "normed = rmsnorm(new residual)")
+
+
+def test_fused_add_residual_is_the_rne_bf16_sum():
+    x = _rand(5, 4096, dtype=torch.bfloat16, seed=6)
+    r = _rand(5, 4096, dtype=torch.bfloat16, seed=7, scale=4.0)
+    _, res = ref.fused_add_rmsnorm(x, r, torch.ones(4096, dtype=torch.bfloat16), 1e-6)
+    want = _round_bf16_np(r.float().numpy() + x.float().numpy())
+    assert np.array_equal(res.float().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_fused_add_does_not_modify_inputs():
+    x = _rand(3, 64, dtype=torch.float16, seed=1)
+    r = _rand(3, 64, dtype=torch.float16, seed=2)
+    xc, rc = x.clone(), r.clone()
+    ref.fused_add_rmsnorm(x, r, torch.ones(64, dtype=torch.float16), 1e-6)
+    assert_bitexact(x, xc)
+    assert_bitexact(r, rc)
+
+
+# ---------------------------------------------------------------- rope
+
+def _complex_rotate(x: torch.Tensor, positions: torch.Tensor, base: float) -> torch.Tensor:
+    """Dims (i, i + D/2) as (re, im), multiplied by exp(i * pos * base^(-2i/D)), in float64
+    (the reference's independent check, tests/test_rope.py:17-27)."""
+    d = x.shape[-1]
+    half = d // 2
+    inv = 1.0 / (base ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    ang = positions.double()[:, None] * inv[None, :]
+    rot = torch.polar(torch.ones_like(ang), ang)
+    z = torch.complex(x[..., :half].double(), x[..., half:].double()) * rot[:, None, :]
+    return torch.cat((z.real, z.imag), dim=-1)
+
+
+def test_rotate_half_on_arange():
+    x = torch.arange(6.0).view(1, 1, 6)
+    assert torch.equal(ref.rotate_half(x), torch.tensor([[[-3.0, -4.0, -5.0, 0.0, 1.0, 2.0]]]))
+
+
+def test_rope_matches_complex_reference():
+    cos, sin = ref.rope_tables(16, 128, 1e4)
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(40, 4, 16, generator=g)
+    k = torch.randn(40, 2, 16, generator=g)
+    pos = torch.randint(0, 128, (40,), generator=g)
+    qo, ko = ref.rope(q, k, cos, sin, pos)
+    torch.testing.assert_close(qo.double(), _complex_rotate(q, pos, 1e4), atol=1e-5, rtol=0)
+    torch.testing.assert_close(ko.double(), _complex_rotate(k, pos, 1e4), atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rope_half_precision_within_one_ulp_of_float64(dtype):
+    """In 16-bit storage the final cast dominates: the result is within 1 ulp (relative)
+    of the float64 rotation of the same inputs, plus an absolute slack for the fp32 angle
+    and product errors, which only matter where the result cancels to near zero."""
+    cos, sin = ref.rope_tables(128, 64, 1e6)
+    q = _rand(30, 8, 128, dtype=dtype, seed=3)
+    pos = torch.randint(0, 64, (30,), generator=torch.Generator().manual_seed(4))
+    qo, _ = ref.rope(q, q[:, :1], cos, sin, pos)
+    one_ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    torch.testing.assert_close(qo.double(), _complex_rotate(q, pos, 1e6), atol=4e-5, rtol=one_ulp)
+
+
+def test_rope_position_zero_is_identity():
+    cos, sin = ref.rope_tables(64, 8, 1e6)
+    q = _rand(5, 4, 64, dtype=torch.bfloat16, seed=5)
+    qo, ko = ref.rope(q, q[:, :2], cos, sin, torch.zeros(5, dtype=torch.int64))
+    assert_bitexact(qo, q)
+    assert_bitexact(ko, q[:, :2])
+
+
+def test_rope_preserves_norm_and_is_relative():
+    cos, sin = ref.rope_tables(16, 128, 1e4)
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(32, 4, 16, generator=g)
+    pos = torch.randint(0, 128, (32,), generator=g)
+    qo, _ = ref.rope(q, q, cos, sin, pos)
+    torch.testing.assert_close(qo.norm(dim=-1), q.norm(dim=-1), atol=1e-5, rtol=0)
+    a = torch.randn(1, 1, 16, generator=g)
+    b = torch.randn(1, 1, 16, generator=g)
+
+    def score(m, n):
+        am, _ = ref.rope(a, a, cos, sin, torch.tensor([m]))
+        bn, _ = ref.rope(b, b, cos, sin, torch.tensor([n]))
+        return (am * bn).sum()
+
+    torch.testing.assert_close(score(10, 3), score(27, 20), atol=1e-5, rtol=0)
+
+
+def test_rope_tables_against_float64():
+    cos, sin = ref.rope_tables(128, 4096, 1e6)
+    assert cos.shape == (4096, 128) and cos.dtype == torch.float32
+    assert torch.equal(cos[:, :64], cos[:, 64:]) and torch.equal(sin[:, :64], sin[:, 64:])
+    inv32 = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).double()
+    ang = torch.arange(4096, dtype=torch.float64)[:, None] * inv32[None, :]
+    # fp32 angle products carry ~pos * 2^-24 absolute error; cos/sin within that plus 1 ulp
+    tol = 4096 * 2.0 ** -23
+    torch.testing.assert_close(cos[:, :64].double(), torch.cos(ang), atol=tol, rtol=0)
+    torch.testing.assert_close(sin[:, :64].double(), torch.sin(ang), atol=tol, rtol=0)
+
+
+def test_llama3_scaling_bands():
+    """High frequencies kept, low frequencies divided by `factor`, monotone in between
+    (the reference checks the same bands, tests/test_model_families.py:70-90)."""
+    sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    out = ref.llama3_scale_inv_freq(inv, sc)
+    wavelen = 2 * math.pi / inv
+    hi = wavelen < 8192 / 4
+    lo = wavelen > 8192 / 1
+    assert torch.equal(out[hi], inv[hi])
+    torch.testing.assert_close(out[lo], inv[lo] / 8)
+    mid = ~hi & ~lo
+    assert bool(((out[mid] <= inv[mid]) & (out[mid] >= inv[mid] / 8)).all())
+
+
+# ---------------------------------------------------------------- silu
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_silu_and_mul_matches_float64(dtype):
+    x = _rand(3, 2 * 4864, dtype=dtype, seed=7, scale=2.0)
+    got = ref.silu_and_mul(x)
+    g, u = x[:, :4864].double(), x[:, 4864:].double()
+    act = (g / (1 + torch.exp(-g))).to(dtype).double()  # rounded before the multiply
+    assert_ulp(got, (act * u).to(dtype), 1, "silu vs float64")
+
+
+def test_silu_special_values():
+    x = torch.tensor([[0.0, 20.0, -20.0, 1.0, 3.0, 3.0, 2.0, -1.0]], dtype=torch.float32)
+    out = ref.silu_and_mul(x)
+    assert out[0, 0] == 0.0
+    torch.testing.assert_close(out[0, 1], torch.tensor(20.0 * 3.0), rtol=1e-7, atol=0)  # ~g*u
+    assert abs(float(out[0, 2])) < 1e-6  # silu(-20) ~ -4e-8, times 2
+    torch.testing.assert_close(out[0, 3], torch.tensor(1.0 / (1 + math.exp(-1.0)) * -1.0))
+
+
+# ---------------------------------------------------------------- embedding
+
+def test_embedding_matches_numpy_take():
+    ids, w = gen.embedding_inputs(300, 1000, 96, torch.bfloat16, seed=2)
+    got = ref.embedding(ids, w)
+    want = np.take(w.view(torch.int16).numpy(), ids.numpy(), axis=0)
+    assert np.array_equal(got.view(torch.int16).numpy(), want)
+
+
+def test_embedding_rejects_out_of_range():
+    w = torch.zeros(10, 4)
+    with pytest.raises(IndexError):
+        ref.embedding(torch.tensor([10]), w)
+
+
+# ---------------------------------------------------------------- composed ops
+
+def test_qk_norm_rope_matches_float64():
+    n, hq, hk, d = 12, 4, 2, 128
+    qkv, qw, kw, pos = gen.qkv_inputs(n, hq, hk, d, 64, torch.bfloat16, seed=50)
+    cos, sin = ref.rope_tables(d, 64, 1e6)
+    q = qkv[:, :hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    qo, ko = ref.qk_norm_rope(q, k, qw, kw, 1e-6, cos, sin, pos)
+    for x, w, o in [(q, qw, qo), (k, kw, ko)]:
+        y = _rmsnorm_f64(x.reshape(-1, d), w, 1e-6).view(x.shape)  # bf16, as the model stores it
+        want = _complex_rotate(y, pos, 1e6).to(torch.bfloat16)
+        assert ulp_diff(o, want).max() <= 2
+
+
+def test_mla_latent_rope_matches_float64():
+    n, h, dn, dr, r = 10, 4, 32, 64, 512
+    kv_a, q, w, pos = gen.mla_inputs(n, h, dn, dr, r, 256, torch.bfloat16, seed=61)
+    cos, sin = ref.rope_tables(dr, 256, 5e4)
+    qv = q.view(n, h, dn + dr)
+    q_pe, latent = ref.mla_latent_rope(kv_a[:, :r], kv_a[:, r:], qv[..., dn:], w, 1e-6, cos, sin, pos)
+    assert latent.shape == (n, r + dr)
+    assert_ulp(latent[:, :r], _rmsnorm_f64(kv_a[:, :r], w, 1e-6), 1, "latent c")
+    want_k = _complex_rotate(kv_a[:, r:].unsqueeze(1), pos, 5e4).squeeze(1).to(torch.bfloat16)
+    assert ulp_diff(latent[:, r:], want_k).max() <= 1
+    want_q = _complex_rotate(qv[..., dn:], pos, 5e4).to(torch.bfloat16)
+    assert ulp_diff(q_pe, want_q).max() <= 1
+
+
+def test_ulp_helper_counts_ulps():
+    a = torch.tensor([1.0, -1.0, 0.0], dtype=torch.float16)
+    b = torch.tensor([1.0 + 2 ** -10, -1.0 - 2 * 2 ** -10, -0.0], dtype=torch.float16)
+    assert ulp_diff(a, b).tolist() == [1, 2, 0]
