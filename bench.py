@@ -1,0 +1,425 @@
+"""Benchmark of the fused per-layer ops on one MI355X.
+
+Step (the timed unit): one pass of the Qwen3-8B per-layer elementwise chain at the prefill
+shape T = 8192: embedding gather from the [151936, 4096] bf16 table,
+Qwen3 QK-RMSNorm + neox rope on the fused qkv output (32 q + 8 kv heads x 128), and the
+residual-add + RMSNorm at hidden 4096. Inputs are resident in HBM; consecutive steps
+rotate through enough input sets (> 1 GiB) that no step finds its data in the 256 MB
+Infinity Cache. `value` = algorithmic bytes of the chain / time per step (GB/s).
+
+Also printed in the same JSON line:
+  per_op        every BASELINE configuration: GPU us per launch, achieved GB/s, % of
+                8 TB/s (algorithmic bytes; inputs rotated past the Infinity Cache;
+                back-to-back launches timed with hipEvents)
+  us_per_layer  config 4 summed per T, plus the full per-layer elementwise set
+  roofline      the dominant kernel of the step (add+RMSNorm, T=8192), timed live with
+                hipEvents on its launch stream inside the timed region
+  cpu_baseline  the CPU oracle (the reference's PyTorch-eager ops restated) on a bounded
+                sample of the same chain on this host
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--only OP]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PEAK_GBPS = 8000.0
+METRIC = "achieved HBM GB/s (% of MI355X peak) per fused op; µs per layer at 7B"
+ROTATE_BYTES = 1.5 * 2 ** 30  # input sets rotated per op: > 5x the Infinity Cache
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- workloads
+
+class Op:
+    """A benchmarked launch: `make(i)` builds input set i on the GPU, `run(args)` launches."""
+
+    def __init__(self, name, config, shape, nbytes, make, run, footprint):
+        self.name, self.config, self.shape, self.nbytes = name, config, shape, nbytes
+        self.make, self.run, self.footprint = make, run, footprint
+
+
+def _ops(torch, ops, tables):
+    dev = torch.device("cuda")
+    bf, f16 = torch.bfloat16, torch.float16
+    g = torch.Generator(device=dev)
+
+    def randn(shape, dtype, seed, mean=0.0, std=1.0):
+        g.manual_seed(seed)
+        return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
+
+    def randint(n, high, seed):
+        g.manual_seed(seed)
+        return torch.randint(0, high, (n,), generator=g, device=dev)
+
+    out = []
+
+    def add_norm(cfg, t, h, dtype):
+        def make(i):
+            return (randn((t, h), dtype, 3 * i), randn((t, h), dtype, 3 * i + 1),
+                    randn((h,), dtype, 3 * i + 2, 1.0, 0.1))
+        nbytes = 4 * t * h * 2 + h * 2
+        out.append(Op("add_rmsnorm", cfg, f"[{t},{h}] {str(dtype)[6:]}", nbytes, make,
+                      lambda a: ops.fused_add_rmsnorm_hip(a[0], a[1], a[2], 1e-6), 4 * t * h * 2))
+
+    def rope(cfg, t):
+        cos, sin = tables(128, 32768, 1e6)
+
+        def make(i):
+            return (randn((t, 28, 128), bf, 3 * i), randn((t, 4, 128), bf, 3 * i + 1),
+                    randint(t, 32768, 3 * i + 2))
+        nbytes = 2 * t * 32 * 128 * 2 + 8 * t
+        out.append(Op("rope", cfg, f"q[{t},28,128] k[{t},4,128] bf16", nbytes, make,
+                      lambda a: ops.rope_hip(a[0], a[1], cos, sin, a[2]), nbytes))
+
+    def silu(cfg, t, inter=18944, dtype=f16, label="silu_and_mul"):
+        def make(i):
+            return (randn((t, 2 * inter), dtype, i, 0.0, 2.0),)
+        nbytes = 3 * t * inter * 2
+        out.append(Op(label, cfg, f"[{t},{2 * inter}] {str(dtype)[6:]}", nbytes, make,
+                      lambda a: ops.silu_and_mul_hip(a[0]), nbytes))
+
+    table_cache = {}
+
+    def embedding(cfg, t):
+        def make(i):
+            if "w" not in table_cache:
+                table_cache["w"] = randn((151936, 4096), bf, 999, 0.0, 0.02)
+            return (randint(t, 151936, i), table_cache["w"])
+        nbytes = t * (8 + 2 * 4096 * 2)
+        out.append(Op("embedding", cfg, f"table[151936,4096] bf16, T={t}", nbytes, make,
+                      lambda a: ops.embedding_hip(a[0], a[1]), nbytes))
+
+    def qk(cfg, t):
+        cos, sin = tables(128, 40960, 1e6)
+
+        def make(i):
+            qkv = randn((t, 6144), bf, 4 * i)
+            return (qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128),
+                    randn((128,), bf, 4 * i + 1, 1.0, 0.1), randn((128,), bf, 4 * i + 2, 1.0, 0.1),
+                    randint(t, 40960, 4 * i + 3), qkv)
+        nbytes = 2 * t * 40 * 128 * 2 + 8 * t + 2 * 128 * 2
+        out.append(Op("qk_norm_rope", cfg, f"qkv[{t},6144] 32q+8kv x128 bf16", nbytes, make,
+                      lambda a: ops.qk_norm_rope_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4]),
+                      t * 6144 * 2))
+
+    def mla(cfg, t, in_model):
+        cos, sin = tables(64, 8192, 5e4)
+
+        def make(i):
+            kv_a = randn((t, 576), bf, 4 * i)
+            q = randn((t, 16, 192), bf, 4 * i + 1)
+            if in_model:
+                buf = torch.cat([q.view(t, 3072), kv_a], dim=-1)
+                q = buf[:, :3072].view(t, 16, 192)
+                kv_a = buf[:, 3072:]
+            return (kv_a[:, :512], kv_a[:, 512:], q[..., 128:], randn((512,), bf, 4 * i + 2, 1.0, 0.1),
+                    randint(t, 8192, 4 * i + 3))
+        nbytes = t * 6408 + 1024
+        layout = "views of one [T,3648] row" if in_model else "separate tensors"
+        out.append(Op("mla_latent_rope", cfg, f"kv_a[{t},576] q[{t},16,192] bf16 ({layout})", nbytes, make,
+                      lambda a: ops.mla_latent_rope_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4]),
+                      t * (576 + 3072 + 576) * 2))
+
+    add_norm("1", 256, 896, f16)
+    rope("2", 256)
+    rope("2", 4096)
+    for t in (1, 256, 8192):
+        silu("3", t)
+    for t in (256, 8192):
+        embedding("4a", t)
+        qk("4b", t)
+        add_norm("4c", t, 4096, bf)
+    mla("5", 8192, False)
+    mla("5", 8192, True)
+    silu("extra", 8192, inter=12288, dtype=bf, label="silu_and_mul")  # Qwen3-8B MLP
+    return out
+
+
+_US_PER_SLEEP_CYCLE = None
+
+
+def _sleep_us(torch, us):
+    """Occupies the stream for about `us` microseconds (torch's spin kernel), so that the
+    launches queued behind it start back to back, independent of host launch cost."""
+    global _US_PER_SLEEP_CYCLE
+    if _US_PER_SLEEP_CYCLE is None:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize()
+        a.record()
+        torch.cuda._sleep(1_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _US_PER_SLEEP_CYCLE = a.elapsed_time(b) * 1e3 / 1_000_000
+    torch.cuda._sleep(int(us / _US_PER_SLEEP_CYCLE))
+
+
+def _time_op(torch, op, reps, launches=16):
+    """GPU time per launch of `op`. Each rep queues `launches` launches (rotating over
+    input sets, so a launch's data was last touched more than ROTATE_BYTES of traffic
+    earlier) behind a GPU spin long enough for the host to enqueue them all; hipEvents
+    around the launches then see back-to-back kernels, not the host's per-launch cost
+    (Python + ctypes, ~15 us, which is what a 1-10 us kernel would otherwise measure).
+    Returns the median over reps of (elapsed / launches)."""
+    nsets = max(2, min(512, math.ceil(ROTATE_BYTES / max(op.footprint, 1))))
+    sets = [op.make(i) for i in range(nsets)]
+    for a in sets:  # first touch + warm the launch path
+        op.run(a)
+    torch.cuda.synchronize()
+    reps = max(8, reps // launches)
+    us = []
+    k = 0
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        _sleep_us(torch, 40.0 * launches)
+        start.record()
+        for _ in range(launches):
+            op.run(sets[k % nsets])
+            k += 1
+        end.record()
+        torch.cuda.synchronize()
+        us.append(start.elapsed_time(end) * 1e3 / launches)
+    del sets
+    return statistics.median(us), nsets
+
+
+# ----------------------------------------------------------------------------- chain step
+
+def _chain_sets(torch, t, nsets):
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(12345)
+    table = (torch.randn((151936, 4096), generator=g, device=dev) * 0.02).to(bf)
+    sets = []
+    for i in range(nsets):
+        g.manual_seed(100 + i)
+        sets.append(dict(
+            ids=torch.randint(0, 151936, (t,), generator=g, device=dev),
+            qkv=torch.randn((t, 6144), generator=g, device=dev).to(bf),
+            qw=(torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf),
+            kw=(torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf),
+            pos=torch.randint(0, 40960, (t,), generator=g, device=dev),
+            x=torch.randn((t, 4096), generator=g, device=dev).to(bf),
+            r=torch.randn((t, 4096), generator=g, device=dev).to(bf),
+            w=(torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)))
+    return table, sets
+
+
+def _chain_bytes(t):
+    return t * (8 + 2 * 4096 * 2) + (2 * t * 40 * 128 * 2 + 8 * t + 512) + (8 * t * 4096 + 4096 * 2)
+
+
+def _run_chain(ops, t, table, s, cos, sin):
+    ops.embedding_hip(s["ids"], table)
+    qkv = s["qkv"]
+    ops.qk_norm_rope_hip(qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), s["qw"], s["kw"],
+                         1e-6, cos, sin, s["pos"])
+    return ops.fused_add_rmsnorm_hip(s["x"], s["r"], s["w"], 1e-6)
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+def _cpu_baseline(t, budget_s):
+    """The oracle (torch CPU eager, the reference's ops restated) on the same chain: the
+    embedding gather, Qwen3 qk-norm + rope, and add + RMSNorm at T tokens, hidden 4096."""
+    import torch
+
+    from oracle import inputs as gen
+    from oracle import ref_ops as ref
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    ids, table = gen.embedding_inputs(t, 151936, 4096, torch.bfloat16, seed=1)
+    qkv, qw, kw, pos = gen.qkv_inputs(t, 32, 8, 128, 40960, torch.bfloat16, seed=2)
+    x, r, w = gen.add_rmsnorm_inputs(t, 4096, torch.bfloat16, seed=3)
+    cos, sin = ref.rope_tables(128, 40960, 1e6)
+    q, k = qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128)
+
+    def step():
+        ref.embedding(ids, table)
+        ref.qk_norm_rope(q, k, qw, kw, 1e-6, cos, sin, pos)
+        ref.fused_add_rmsnorm(x, r, w, 1e-6)
+
+    step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {"value": round(_chain_bytes(t) / sec / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_step": round(sec * 1e3, 2),
+            "sample": f"Qwen3-8B chain (embedding + qk-norm/rope + add+RMSNorm) at T={t}, "
+                      f"median of {len(times)} reps after 1 warm-up, torch {torch.__version__} CPU eager"}
+
+
+# ----------------------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--reps", type=int, default=256, help="launches per op in the per-op table")
+    ap.add_argument("--quick", action="store_true", help="skip the per-op table and the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run only this op's per-op rows (for profiler runs)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only; every op is row-independent and shards "
+              "over tokens with no exchange (see DESIGN.md), so --gpus must be 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from emberserve_amd import _lib, ops
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    _lib.load()
+    torch.cuda.init()
+
+    table_cache = {}
+
+    def tables(d, max_pos, theta):
+        key = (d, max_pos, theta)
+        if key not in table_cache:
+            from emberserve_amd.rope import RotaryEmbedding
+            table_cache[key] = RotaryEmbedding(d, max_pos, theta).full_tables(torch.device("cuda"))
+        return table_cache[key]
+
+    result = {}
+    per_op = []
+    if not args.quick:
+        for op in _ops(torch, ops, tables):
+            if args.only and op.name != args.only:
+                continue
+            _log(f"per-op: {op.name} cfg {op.config} {op.shape}")
+            us, nsets = _time_op(torch, op, args.reps)
+            gbps = op.nbytes / (us * 1e-6) / 1e9
+            per_op.append({"op": op.name, "config": op.config, "shape": op.shape, "bytes": op.nbytes,
+                           "us": round(us, 2), "GB/s": round(gbps, 1),
+                           "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "input_sets": nsets})
+            torch.cuda.empty_cache()
+        if args.only:
+            print(json.dumps({"per_op": per_op}))
+            return 0
+
+    # ---- the timed step: config 4 chain at T = 8192 -----------------------------------
+    t = 8192
+    nsets = 4  # ~480 MB of inputs per set: the set a step reads was last touched 3 steps back
+    _log(f"chain: building {nsets} input sets")
+    table, sets = _chain_sets(torch, t, nsets)
+    cos, sin = tables(128, 40960, 1e6)
+    stream = torch.cuda.current_stream()
+    for i in range(args.warmup):
+        _run_chain(ops, t, table, sets[i % nsets], cos, sin)
+    torch.cuda.synchronize()
+    k = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(k)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(k):
+        s = sets[i % nsets]
+        e = ev[i]
+        e[0].record(stream)
+        ops.embedding_hip(s["ids"], table)
+        e[1].record(stream)
+        qkv = s["qkv"]
+        ops.qk_norm_rope_hip(qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), s["qw"],
+                             s["kw"], 1e-6, cos, sin, s["pos"])
+        e[2].record(stream)
+        ops.fused_add_rmsnorm_hip(s["x"], s["r"], s["w"], 1e-6)
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    seg = [[ev[i][j].elapsed_time(ev[i][j + 1]) * 1e3 for i in range(k)] for j in range(3)]
+    step_us = [ev[i][0].elapsed_time(ev[i][3]) * 1e3 for i in range(k)]
+    ms_per_step = wall * 1e3 / k
+    chain_bytes = _chain_bytes(t)
+    gpu_step_us = statistics.mean(step_us)
+    value = chain_bytes / (ms_per_step * 1e-3) / 1e9
+
+    add_bytes = 8 * t * 4096 + 4096 * 2
+    add_us = statistics.mean(seg[2])
+    achieved = add_bytes / (add_us * 1e-6) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("add_rmsnorm_T8192_bytes")
+        except (ValueError, OSError):
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
+                "kernel": "k_rmsnorm<bf16, RESID> (fused residual add + RMSNorm), [8192, 4096] bf16",
+                "bytes_per_launch": add_bytes, "avg_launch_us": round(add_us, 2)}
+    del sets, table
+    torch.cuda.empty_cache()
+
+    # ---- per-layer sums ------------------------------------------------------------------
+    def row(name, cfg, tt):
+        for r in per_op:
+            if r["op"] == name and r["config"] == cfg and (f"T={tt}" in r["shape"] or f"[{tt}," in r["shape"]):
+                return r["us"]
+        return None
+
+    us_per_layer = {}
+    if per_op:
+        for tt in (256, 8192):
+            parts = [row("embedding", "4a", tt), row("qk_norm_rope", "4b", tt), row("add_rmsnorm", "4c", tt)]
+            if all(p is not None for p in parts):
+                us_per_layer[f"qwen3_8b_chain_T{tt}"] = round(sum(parts), 2)
+        parts = [row("add_rmsnorm", "4c", 8192), row("add_rmsnorm", "4c", 8192), row("qk_norm_rope", "4b", 8192),
+                 row("silu_and_mul", "extra", 8192)]
+        if all(p is not None for p in parts):
+            us_per_layer["qwen3_8b_full_elementwise_set_T8192"] = round(sum(parts), 2)
+
+    cpu = None
+    if not args.quick and not args.no_cpu:
+        _log("cpu baseline")
+        cpu = _cpu_baseline(8192, budget_s=20.0)
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": k,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) table, uniform ids/positions)",
+        "config": {"workload": "Qwen3-8B per-layer elementwise chain (BASELINE config 4): embedding gather "
+                               "[151936,4096] + QK-RMSNorm/neox rope (32q+8kv x128, theta 1e6) + "
+                               "residual-add+RMSNorm [T,4096], bf16",
+                   "tokens": t, "bytes_per_step": chain_bytes,
+                   "gpu_us_per_step": round(gpu_step_us, 2),
+                   "pct_peak": round(100 * value / PEAK_GBPS, 1)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "us_per_layer": us_per_layer,
+        "per_op": per_op,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -3,12 +3,20 @@
 // Reference: torch.nn.Embedding.forward as called by emberserve/model/qwen2.py:182 and
 // deepseek.py:205 (F.embedding without max_norm / padding_idx effects on the forward).
 //
-// Work mapping: one wave64 per token. The row is copied in 16-byte units when row bytes,
-// strides and base pointers allow it (else 8/4/2/1-byte units); each lane keeps U units in
-// flight, so a 8 KiB row (hidden 4096, bf16) is one round of 8 dwordx4 loads per lane.
+// Work mapping: a team of TPR lanes per token. The row is copied in 16-byte units when row
+// bytes, strides and base pointers allow it (else 8/4/2/1-byte units); each lane keeps U
+// units in flight, so with TPR = 128 and U = 4 a 8 KiB row (hidden 4096, bf16) is one
+// round of 4 dwordx4 loads per lane (measured best of TPR 64/128/256 x U 2/4/8).
 // An id outside [0, vocab) writes a zero row and sets EMBER_ERR_EMBED_ID; it never reads
 // outside the table.
 #include "ember_common.h"
+
+#ifndef EMBER_EMB_U
+#define EMBER_EMB_U 4
+#endif
+#ifndef EMBER_EMB_TPR
+#define EMBER_EMB_TPR 128
+#endif
 
 namespace ember {
 namespace {
@@ -36,32 +44,51 @@ struct Unit<1> {
   using type = uint8_t;
 };
 
-template <int VB, int U>
+// 16-byte units stream (the gathered rows are read once, the output written once).
+template <typename V>
+__device__ __forceinline__ V load_unit(const V* p) {
+  if constexpr (sizeof(V) == 16) {
+    return __builtin_bit_cast(V, load_stream<uint32_t, 4>(reinterpret_cast<const uint32_t*>(p)));
+  } else {
+    return *p;
+  }
+}
+
+template <typename V>
+__device__ __forceinline__ void store_unit(V* p, const V& v) {
+  if constexpr (sizeof(V) == 16) {
+    store_stream<uint32_t, 4>(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(Pack<uint32_t, 4>, v));
+  } else {
+    *p = v;
+  }
+}
+
+template <int VB, int U, int TPR>
 __global__ void __launch_bounds__(256)
 k_embedding(const int64_t* __restrict__ ids, int64_t ntok, const uint8_t* __restrict__ w, int64_t vocab,
             int64_t w_stride_bytes, uint8_t* __restrict__ out, int64_t out_stride_bytes, int nunits,
             uint32_t* __restrict__ err) {
   using V = typename Unit<VB>::type;
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * (256 / TPR) + threadIdx.x / TPR;
+  const int lane = threadIdx.x % TPR;
   if (tok >= ntok) return;
   const int64_t id = ids[tok];
   V* dst = reinterpret_cast<V*>(out + tok * out_stride_bytes);
   if (id < 0 || id >= vocab) {
     if (lane == 0) atomicOr(err, EMBER_ERR_EMBED_ID);
     V zero{};
-    for (int i = lane; i < nunits; i += kWave) dst[i] = zero;
+    for (int i = lane; i < nunits; i += TPR) dst[i] = zero;
     return;
   }
   const V* src = reinterpret_cast<const V*>(w + id * w_stride_bytes);
-  for (int base = 0; base < nunits; base += kWave * U) {
+  for (int base = 0; base < nunits; base += TPR * U) {
     V buf[U];
 #pragma unroll
-    for (int k = 0; k < U; ++k) buf[k] = src[min(base + lane + k * kWave, nunits - 1)];
+    for (int k = 0; k < U; ++k) buf[k] = load_unit(src + min(base + lane + k * TPR, nunits - 1));
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const int i = base + lane + k * kWave;
-      if (i < nunits) dst[i] = buf[k];
+      const int i = base + lane + k * TPR;
+      if (i < nunits) store_unit(dst + i, buf[k]);
     }
   }
 }
@@ -70,9 +97,10 @@ template <int VB>
 int launch_vb(const int64_t* ids, int64_t ntok, const void* w, int64_t vocab, int64_t wsb, void* out,
               int64_t osb, int64_t row_bytes, uint32_t* err, hipStream_t stream) {
   const int64_t nunits = row_bytes / VB;
-  const int64_t grid = cdiv(ntok, 4);
+  constexpr int kTpr = EMBER_EMB_TPR;
+  const int64_t grid = cdiv(ntok, 256 / kTpr);
   if (grid > 0x7fffffffLL || nunits > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_embedding<VB, 8>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, ids, ntok,
+  hipLaunchKernelGGL((k_embedding<VB, EMBER_EMB_U, kTpr>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, ids, ntok,
                      static_cast<const uint8_t*>(w), vocab, wsb, static_cast<uint8_t*>(out), osb,
                      static_cast<int>(nunits), err);
   return launch_status();

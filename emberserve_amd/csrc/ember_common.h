@@ -50,6 +50,32 @@ __device__ __forceinline__ void store_pack(T* p, const Pack<T, N>& v) {
   *reinterpret_cast<Pack<T, N>*>(p) = v;
 }
 
+// Streaming (non-temporal) 16-byte accesses for data touched exactly once per launch
+// (activations read, rows written): the nt hint keeps these lines from displacing reused
+// data (weights, cos/sin tables, positions) in L2 and the Infinity Cache. Measured on
+// MI355X: +13-17% HBM throughput for the in-place rope and the copy-like kernels. Packs of
+// other sizes (the scalar fallback kernels) use ordinary accesses.
+template <typename T, int N>
+__device__ __forceinline__ Pack<T, N> load_stream(const T* p) {
+  if constexpr (sizeof(T) * N == 16) {
+    using V = unsigned int __attribute__((ext_vector_type(4)));
+    const V v = __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+    return __builtin_bit_cast(Pack<T, N>, v);
+  } else {
+    return load_pack<T, N>(p);
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_stream(T* p, const Pack<T, N>& v) {
+  if constexpr (sizeof(T) * N == 16) {
+    using V = unsigned int __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(__builtin_bit_cast(V, v), reinterpret_cast<V*>(p));
+  } else {
+    store_pack<T, N>(p, v);
+  }
+}
+
 // Loads N consecutive values of type T (16-byte aligned when N * sizeof(T) >= 16) as fp32.
 template <typename T, int N>
 __device__ __forceinline__ void load_vals(const T* p, float (&out)[N]) {

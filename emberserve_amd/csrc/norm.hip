@@ -40,8 +40,8 @@ k_rmsnorm(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int64_t 
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int vi = min(lane + i * TPR, nvec - 1);
-    a[i] = load_pack<T, VEC>(x + lrow * xs + static_cast<int64_t>(vi) * VEC);
-    if constexpr (RESID) b[i] = load_pack<T, VEC>(r + lrow * rs + static_cast<int64_t>(vi) * VEC);
+    a[i] = load_stream<T, VEC>(x + lrow * xs + static_cast<int64_t>(vi) * VEC);
+    if constexpr (RESID) b[i] = load_stream<T, VEC>(r + lrow * rs + static_cast<int64_t>(vi) * VEC);
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -69,7 +69,7 @@ k_rmsnorm(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int64_t 
       ss += f * f;
     }
     if constexpr (RESID) {
-      if (ok) store_pack<T, VEC>(rout + row * ros + static_cast<int64_t>(vi) * VEC, s);
+      if (ok) store_stream<T, VEC>(rout + row * ros + static_cast<int64_t>(vi) * VEC, s);
     }
   }
 
@@ -99,7 +99,7 @@ k_rmsnorm(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int64_t 
         const float y = round_to<T>(v[i][e] * inv);
         o.v[e] = from_f32<T>(y * wv[i][e]);
       }
-      store_pack<T, VEC>(out + row * os + static_cast<int64_t>(vi) * VEC, o);
+      store_stream<T, VEC>(out + row * os + static_cast<int64_t>(vi) * VEC, o);
     }
   }
 }
@@ -194,8 +194,13 @@ int launch_tpr(const NormArgs& a, int tpr, int nv) {
   }
 }
 
-// Threads wanted in flight before a row team is widened no further (2 waves per SIMD).
-constexpr int64_t kTargetThreads = 131072;
+// Row teams are widened (fewer packs per lane) until a launch has this many lanes or the
+// team reaches one pack per lane. Measured on MI355X ([8192, 4096] bf16 fused add): 64
+// lanes x 8 packs 69%, 256 x 2 74%, 512 x 1 76% of HBM peak.
+#ifndef EMBER_NORM_TARGET_THREADS
+#define EMBER_NORM_TARGET_THREADS 4194304
+#endif
+constexpr int64_t kTargetThreads = EMBER_NORM_TARGET_THREADS;
 
 // Picks the row-team width: the narrowest team that holds the row in <= 8 packs per lane,
 // widened (fewer packs per lane) while the launch would have too few threads in flight.

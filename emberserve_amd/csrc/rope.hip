@@ -21,6 +21,10 @@
 // packs once for all of them. The qk-norm sum of squares is a J-lane DPP reduction.
 #include "ember_common.h"
 
+#ifndef EMBER_ROPE_G1_MAX_THREADS
+#define EMBER_ROPE_G1_MAX_THREADS (int64_t(1) << 26)
+#endif
+
 namespace ember {
 namespace {
 
@@ -37,14 +41,11 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
   const uint32_t tok = gdiv.div(rowid);
   if (tok >= ntok) return;  // whole J-lane groups leave together
   const uint32_t hg = rowid - tok * ngroups;
-  const int64_t p = pos[tok];
-  if (p < 0 || p >= trows) {
-    if (j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
-    return;
-  }
   const int nh = hq + hk;
   const int64_t off = static_cast<int64_t>(j) * VEC;
 
+  // The head rows are loaded before the position is checked, so their HBM latency overlaps
+  // the position -> c/s table chain instead of following it.
   Pack<T, VEC> x1[G];
   Pack<T, VEC> x2[G];
   T* ptr[G];
@@ -52,21 +53,41 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
   for (int g = 0; g < G; ++g) {
     const int h = min(static_cast<int>(hg) * G + g, nh - 1);
     ptr[g] = (h < hq ? q + tok * qts + h * qhs : k + tok * kts + (h - hq) * khs) + off;
-    x1[g] = load_pack<T, VEC>(ptr[g]);
-    x2[g] = load_pack<T, VEC>(ptr[g] + half);
+    x1[g] = load_stream<T, VEC>(ptr[g]);
+    x2[g] = load_stream<T, VEC>(ptr[g] + half);
   }
+  const int64_t p = pos[tok];
+  const bool bad = p < 0 || p >= trows;
+  const int64_t pc = bad ? 0 : p;
   float c[VEC];
   float s[VEC];
-  load_vals<float, VEC>(cos_t + p * tstride + off, c);
-  load_vals<float, VEC>(sin_t + p * tstride + off, s);
+  load_vals<float, VEC>(cos_t + pc * tstride + off, c);
+  load_vals<float, VEC>(sin_t + pc * tstride + off, s);
+  // Norm weights: a lane's heads are all q or, past the q heads, mostly k; load the q
+  // weight packs and, only when some of its heads are k heads, the k weight packs.
   float wq1[VEC], wq2[VEC], wk1[VEC], wk2[VEC];
   if constexpr (NORM) {
-    load_vals<WT, VEC>(qw + off, wq1);
-    load_vals<WT, VEC>(qw + half + off, wq2);
-    load_vals<WT, VEC>(kw + off, wk1);
-    load_vals<WT, VEC>(kw + half + off, wk2);
+    const bool any_q = static_cast<int>(hg) * G < hq;
+    const bool any_k = static_cast<int>(hg) * G + G - 1 >= hq;
+    const WT* w0 = any_q ? qw : kw;
+    load_vals<WT, VEC>(w0 + off, wq1);
+    load_vals<WT, VEC>(w0 + half + off, wq2);
+    if (any_q && any_k) {
+      load_vals<WT, VEC>(kw + off, wk1);
+      load_vals<WT, VEC>(kw + half + off, wk2);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        wk1[e] = wq1[e];
+        wk2[e] = wq2[e];
+      }
+    }
   }
 
+  if (bad) {  // an out-of-range position leaves the token's rows untouched
+    if (j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int h = static_cast<int>(hg) * G + g;
@@ -98,8 +119,8 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
         o1.v[e] = from_f32<T>(f1[e] * c[e] - f2[e] * s[e]);
         o2.v[e] = from_f32<T>(f2[e] * c[e] + f1[e] * s[e]);
       }
-      store_pack<T, VEC>(ptr[g], o1);
-      store_pack<T, VEC>(ptr[g] + half, o2);
+      store_stream<T, VEC>(ptr[g], o1);
+      store_stream<T, VEC>(ptr[g] + half, o2);
     }
   }
 }
@@ -185,12 +206,13 @@ int launch_vec(const RopeArgs& a) {
 
 template <typename T, typename WT, int VEC, int J, bool NORM>
 int launch_g(const RopeArgs& a) {
-  // Heads per lane: as many as keep >= 2^17 lanes busy (up to 4), so large batches get
-  // more loads in flight per lane and fewer c/s table reads.
+  // Heads per lane. Measured on MI355X (rope, T = 4096-16384): one head per lane beats
+  // two or four (more waves in flight outweigh the extra c/s table reads), so G > 1 is
+  // used only when a launch would exceed EMBER_ROPE_G1_MAX_THREADS lanes.
   const int64_t nh = a.hq + a.hk;
-  if (a.ntok * cdiv(nh, 4) * J >= 131072) return launch_vec<T, WT, VEC, J, 4, NORM>(a);
-  if (a.ntok * cdiv(nh, 2) * J >= 131072) return launch_vec<T, WT, VEC, J, 2, NORM>(a);
-  return launch_vec<T, WT, VEC, J, 1, NORM>(a);
+  if (a.ntok * nh * J <= EMBER_ROPE_G1_MAX_THREADS) return launch_vec<T, WT, VEC, J, 1, NORM>(a);
+  if (a.ntok * cdiv(nh, 2) * J <= EMBER_ROPE_G1_MAX_THREADS) return launch_vec<T, WT, VEC, J, 2, NORM>(a);
+  return launch_vec<T, WT, VEC, J, 4, NORM>(a);
 }
 
 template <typename T, typename WT, bool NORM>
@@ -241,114 +263,114 @@ int check_rope_args(const RopeArgs& a) {
 //
 // deepseek.py:124-133 with the rope permutation folded into the weights: per token,
 //   latent[:R] = rmsnorm(c, w), latent[R:R+Dr] = rope(k_pe), q_pe[h] = rope(q_pe[h]).
-// One wave64 per token. The R-wide latent row is held as NVC packs per lane and reduced
-// over the whole wave; the (H + 1) rope head rows (H query heads and the single key head)
-// are J-lane items, two items per lane per round with all their loads issued first.
+// Work is split into independent wave tasks so each wave has one short dependency chain
+// (position -> c/s table) and the launch has twice as many waves in flight: per token, one
+// "latent" wave (the R-wide row as NVC packs per lane, a whole-wave DPP reduction, plus
+// the single key head's rope on its first J lanes) and ceil(H * J / 64) "query" waves (J
+// lanes per query head, 64 / J heads per wave).
 
 template <typename T, typename WT, int VEC, int J, int NVC>
 __global__ void __launch_bounds__(256)
 k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
       int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
       const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
-      const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts,
+      const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts, int tasks_per_tok,
       uint32_t* __restrict__ err) {
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int64_t task = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
+  const int64_t tok = task / tasks_per_tok;  // uniform across the wave
+  const int sub = static_cast<int>(task - tok * tasks_per_tok);
   if (tok >= ntok) return;
-  const int ncv = R / VEC;
+  const int j = lane % J;
+  const int64_t off = static_cast<int64_t>(j) * VEC;
 
-  // Latent row: issue its loads first.
-  Pack<T, VEC> cv[NVC];
-  float wv[NVC][VEC];
+  if (sub == 0) {
+    // Latent row: c packs, weights, and (lanes < J) the key head, all loaded before the
+    // position so the HBM latency overlaps the position -> table chain.
+    const int ncv = R / VEC;
+    Pack<T, VEC> cv[NVC];
+    float wv[NVC][VEC];
 #pragma unroll
-  for (int i = 0; i < NVC; ++i) {
-    const int vi = min(lane + i * kWave, ncv - 1);
-    cv[i] = load_pack<T, VEC>(c + tok * cts + static_cast<int64_t>(vi) * VEC);
-    load_vals<WT, VEC>(w + static_cast<int64_t>(vi) * VEC, wv[i]);
+    for (int i = 0; i < NVC; ++i) {
+      const int vi = min(lane + i * kWave, ncv - 1);
+      cv[i] = load_stream<T, VEC>(c + tok * cts + static_cast<int64_t>(vi) * VEC);
+      load_vals<WT, VEC>(w + static_cast<int64_t>(vi) * VEC, wv[i]);
+    }
+    const Pack<T, VEC> k1 = load_pack<T, VEC>(kpe + tok * kts + off);
+    const Pack<T, VEC> k2 = load_pack<T, VEC>(kpe + tok * kts + half + off);
+    const int64_t p = pos[tok];
+    const bool bad = p < 0 || p >= trows;
+    const int64_t pc = bad ? 0 : p;
+    float cc[VEC], sn[VEC];
+    load_vals<float, VEC>(cos_t + pc * tstride + off, cc);
+    load_vals<float, VEC>(sin_t + pc * tstride + off, sn);
+
+    float v[NVC][VEC];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NVC; ++i) {
+      const bool ok = lane + i * kWave < ncv;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float f = ok ? to_f32(cv[i].v[e]) : 0.f;
+        v[i][e] = f;
+        ss += f * f;
+      }
+    }
+    const float tot = group_sum<kWave>(ss);
+    const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+    T* lrow = lat + tok * lts;
+#pragma unroll
+    for (int i = 0; i < NVC; ++i) {
+      const int vi = lane + i * kWave;
+      if (vi < ncv) {
+        Pack<T, VEC> o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * wv[i][e]);
+        store_stream<T, VEC>(lrow + static_cast<int64_t>(vi) * VEC, o);
+      }
+    }
+    if (lane < J) {
+      Pack<T, VEC> o1, o2;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float f1 = to_f32(k1.v[e]);
+        const float f2 = to_f32(k2.v[e]);
+        // an out-of-range position zeroes the latent key slot (q_pe is left untouched)
+        o1.v[e] = from_f32<T>(bad ? 0.f : f1 * cc[e] - f2 * sn[e]);
+        o2.v[e] = from_f32<T>(bad ? 0.f : f2 * cc[e] + f1 * sn[e]);
+      }
+      store_stream<T, VEC>(lrow + R + off, o1);
+      store_stream<T, VEC>(lrow + R + half + off, o2);
+      if (bad && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+    }
+    return;
   }
+
+  // Query heads (64 / J per wave).
+  constexpr int kHeadsPerWave = kWave / J;
+  const int head = (sub - 1) * kHeadsPerWave + lane / J;
+  if (head >= H) return;  // whole J-lane groups
+  T* ptr = qpe + tok * qts + static_cast<int64_t>(head) * qhs + off;
+  const Pack<T, VEC> a1 = load_stream<T, VEC>(ptr);
+  const Pack<T, VEC> a2 = load_stream<T, VEC>(ptr + half);
   const int64_t p = pos[tok];
   const bool bad = p < 0 || p >= trows;
   const int64_t pc = bad ? 0 : p;
-
-  float v[NVC][VEC];
-  float ss = 0.f;
+  float cc[VEC], sn[VEC];
+  load_vals<float, VEC>(cos_t + pc * tstride + off, cc);
+  load_vals<float, VEC>(sin_t + pc * tstride + off, sn);
+  if (bad) return;  // q_pe untouched; the latent wave reports the error
+  Pack<T, VEC> o1, o2;
 #pragma unroll
-  for (int i = 0; i < NVC; ++i) {
-    const bool ok = lane + i * kWave < ncv;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float f = ok ? to_f32(cv[i].v[e]) : 0.f;
-      v[i][e] = f;
-      ss += f * f;
-    }
+  for (int e = 0; e < VEC; ++e) {
+    const float f1 = to_f32(a1.v[e]);
+    const float f2 = to_f32(a2.v[e]);
+    o1.v[e] = from_f32<T>(f1 * cc[e] - f2 * sn[e]);
+    o2.v[e] = from_f32<T>(f2 * cc[e] + f1 * sn[e]);
   }
-  const float tot = group_sum<kWave>(ss);
-  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
-#pragma unroll
-  for (int i = 0; i < NVC; ++i) {
-    const int vi = lane + i * kWave;
-    if (vi < ncv) {
-      Pack<T, VEC> o;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * wv[i][e]);
-      store_pack<T, VEC>(lat + tok * lts + static_cast<int64_t>(vi) * VEC, o);
-    }
-  }
-
-  if (bad && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
-  const int items = (H + 1) * J;
-  for (int base = 0; base < items; base += 2 * kWave) {
-    Pack<T, VEC> a1[2];
-    Pack<T, VEC> a2[2];
-    float cc[2][VEC];
-    float sn[2][VEC];
-    const T* src[2];
-    T* dst[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int it = min(base + lane + u * kWave, items - 1);
-      const int head = it / J;
-      const int64_t off = static_cast<int64_t>(it % J) * VEC;
-      if (head < H) {
-        T* pq = qpe + tok * qts + static_cast<int64_t>(head) * qhs + off;
-        src[u] = pq;
-        dst[u] = pq;
-      } else {
-        src[u] = kpe + tok * kts + off;
-        dst[u] = lat + tok * lts + R + off;
-      }
-      a1[u] = load_pack<T, VEC>(src[u]);
-      a2[u] = load_pack<T, VEC>(src[u] + half);
-      load_vals<float, VEC>(cos_t + pc * tstride + off, cc[u]);
-      load_vals<float, VEC>(sin_t + pc * tstride + off, sn[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int it = base + lane + u * kWave;
-      if (it < items) {
-        Pack<T, VEC> o1;
-        Pack<T, VEC> o2;
-        if (!bad) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const float f1 = to_f32(a1[u].v[e]);
-            const float f2 = to_f32(a2[u].v[e]);
-            o1.v[e] = from_f32<T>(f1 * cc[u][e] - f2 * sn[u][e]);
-            o2.v[e] = from_f32<T>(f2 * cc[u][e] + f1 * sn[u][e]);
-          }
-          store_pack<T, VEC>(dst[u], o1);
-          store_pack<T, VEC>(dst[u] + half, o2);
-        } else if (it / J >= H) {  // bad position: q_pe untouched, latent key slot zeroed
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            o1.v[e] = from_f32<T>(0.f);
-          }
-          store_pack<T, VEC>(dst[u], o1);
-          store_pack<T, VEC>(dst[u] + half, o1);
-        }
-      }
-    }
-  }
+  store_stream<T, VEC>(ptr, o1);
+  store_stream<T, VEC>(ptr + half, o2);
 }
 
 // Any shape, any alignment: one wave per token, scalar accesses.
@@ -413,12 +435,14 @@ struct MlaArgs {
 
 template <typename T, typename WT, int VEC, int J, int NVC>
 int launch_mla_vec(const MlaArgs& a) {
-  const int64_t grid = cdiv(a.ntok, 4);
+  const int64_t tasks_per_tok = 1 + cdiv(a.H * J, kWave);
+  const int64_t grid = cdiv(a.ntok * tasks_per_tok, 4);
+  if (grid > 0x7fffffffLL) return EMBER_EINVAL;
   hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
                      static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
                      static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2),
                      static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
-                     static_cast<T*>(a.lat), a.lts, a.err);
+                     static_cast<T*>(a.lat), a.lts, static_cast<int>(tasks_per_tok), a.err);
   return launch_status();
 }
 

@@ -10,6 +10,13 @@
 // is issued before the first use. Traffic is the minimum, 3 * I * elem bytes per row.
 #include "ember_common.h"
 
+#ifndef EMBER_SILU_U
+#define EMBER_SILU_U 2
+#endif
+#ifndef EMBER_SILU_MIN_THREADS
+#define EMBER_SILU_MIN_THREADS 131072
+#endif
+
 namespace ember {
 namespace {
 
@@ -29,8 +36,8 @@ k_silu_mul(const T* __restrict__ x, int64_t xs, T* __restrict__ out, int64_t os,
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int64_t vi = min(base + k * 256, nvec - 1);
-    g[k] = load_pack<T, VEC>(xr + vi * VEC);
-    u[k] = load_pack<T, VEC>(xr + inter + vi * VEC);
+    g[k] = load_stream<T, VEC>(xr + vi * VEC);
+    u[k] = load_stream<T, VEC>(xr + inter + vi * VEC);
   }
 #pragma unroll
   for (int k = 0; k < U; ++k) {
@@ -43,7 +50,7 @@ k_silu_mul(const T* __restrict__ x, int64_t xs, T* __restrict__ out, int64_t os,
         const float act = round_to<T>(gf / (1.0f + expf(-gf)));
         o.v[e] = from_f32<T>(act * to_f32(u[k].v[e]));
       }
-      store_pack<T, VEC>(orow + static_cast<int64_t>(vi) * VEC, o);
+      store_stream<T, VEC>(orow + static_cast<int64_t>(vi) * VEC, o);
     }
   }
 }
@@ -67,8 +74,11 @@ int launch_typed(const void* xv, int64_t xs, void* outv, int64_t os, int64_t row
   const bool vec_ok = inter % VEC == 0 && xs % VEC == 0 && os % VEC == 0 && aligned16(x) && aligned16(out);
   if (vec_ok) {
     const int64_t nvec = inter / VEC;
-    // Two packs per lane when the launch is big enough to fill the chip anyway.
-    if (rows * nvec >= 2 * 131072) return launch_vec<T, VEC, 2>(x, xs, out, os, rows, nvec, stream);
+    // More packs per lane only when the launch is big enough to fill the chip anyway.
+    if (EMBER_SILU_U >= 4 && rows * nvec >= 4 * EMBER_SILU_MIN_THREADS)
+      return launch_vec<T, VEC, 4>(x, xs, out, os, rows, nvec, stream);
+    if (EMBER_SILU_U >= 2 && rows * nvec >= 2 * EMBER_SILU_MIN_THREADS)
+      return launch_vec<T, VEC, 2>(x, xs, out, os, rows, nvec, stream);
     return launch_vec<T, VEC, 1>(x, xs, out, os, rows, nvec, stream);
   }
   return launch_vec<T, 1, 1>(x, xs, out, os, rows, inter, stream);
