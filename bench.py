@@ -13,7 +13,7 @@ Also printed in the same JSON line:
                 back-to-back launches timed with hipEvents)
   us_per_layer  config 4 summed per T, plus the full per-layer elementwise set
   roofline      the dominant kernel of the step (add+RMSNorm, T=8192), timed live with
-                hipEvents on its launch stream inside the timed region
+                hipEvents around back-to-back launches on its launch stream
   cpu_baseline  the CPU oracle (the reference's PyTorch-eager ops restated) on a bounded
                 sample of the same chain on this host
 
@@ -145,6 +145,14 @@ def _ops(torch, ops, tables):
     mla("5", 8192, False)
     mla("5", 8192, True)
     silu("extra", 8192, inter=12288, dtype=bf, label="silu_and_mul")  # Qwen3-8B MLP
+
+    # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
+    # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the
+    # counters' bytes-per-unit factor.
+    def copy_cal(i):
+        return (torch.arange(32768, device=dev), randn((32768, 4096), bf, 7000 + i))
+    out.append(Op("copy_calibration", "cal", "identity gather [32768,4096] bf16 (256 MiB)", 2 * 2 ** 28,
+                  copy_cal, lambda a: ops.embedding_hip(a[0], a[1]), 2 * 2 ** 28))
     return out
 
 
@@ -168,14 +176,14 @@ def _sleep_us(torch, us):
     torch.cuda._sleep(int(us / _US_PER_SLEEP_CYCLE))
 
 
-def _time_op(torch, op, reps, launches=16):
+def _time_op(torch, op, reps, launches=16, max_sets=512):
     """GPU time per launch of `op`. Each rep queues `launches` launches (rotating over
     input sets, so a launch's data was last touched more than ROTATE_BYTES of traffic
     earlier) behind a GPU spin long enough for the host to enqueue them all; hipEvents
     around the launches then see back-to-back kernels, not the host's per-launch cost
     (Python + ctypes, ~15 us, which is what a 1-10 us kernel would otherwise measure).
     Returns the median over reps of (elapsed / launches)."""
-    nsets = max(2, min(512, math.ceil(ROTATE_BYTES / max(op.footprint, 1))))
+    nsets = max(2, min(max_sets, math.ceil(ROTATE_BYTES / max(op.footprint, 1))))
     sets = [op.make(i) for i in range(nsets)]
     for a in sets:  # first touch + warm the launch path
         op.run(a)
@@ -270,6 +278,22 @@ def _cpu_baseline(t, budget_s):
                       f"median of {len(times)} reps after 1 warm-up, torch {torch.__version__} CPU eager"}
 
 
+def _profiled_traffic(key):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (profiles/traffic.txt, `key = bytes` lines); None when absent."""
+    f = ROOT / "profiles" / "traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        k, _, v = line.partition("=")
+        if k.strip() == key:
+            try:
+                return int(v.strip())
+            except ValueError:
+                return None
+    return None
+
+
 # ----------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -279,8 +303,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--reps", type=int, default=256, help="launches per op in the per-op table")
     ap.add_argument("--quick", action="store_true", help="skip the per-op table and the CPU baseline")
+    ap.add_argument("--max-sets", type=int, default=512, help="cap on rotated input sets per op (profiler runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None, help="run only this op's per-op rows (for profiler runs)")
+    ap.add_argument("--only", default=None, help="comma list of ops: run only their per-op rows (profiler runs)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -312,11 +337,12 @@ def main() -> int:
     result = {}
     per_op = []
     if not args.quick:
+        only = set(args.only.split(",")) if args.only else None
         for op in _ops(torch, ops, tables):
-            if args.only and op.name != args.only:
+            if (only and op.name not in only) or (not only and op.config == "cal"):
                 continue
             _log(f"per-op: {op.name} cfg {op.config} {op.shape}")
-            us, nsets = _time_op(torch, op, args.reps)
+            us, nsets = _time_op(torch, op, args.reps, max_sets=args.max_sets)
             gbps = op.nbytes / (us * 1e-6) / 1e9
             per_op.append({"op": op.name, "config": op.config, "shape": op.shape, "bytes": op.nbytes,
                            "us": round(us, 2), "GB/s": round(gbps, 1),
@@ -335,47 +361,37 @@ def main() -> int:
     stream = torch.cuda.current_stream()
     for i in range(args.warmup):
         _run_chain(ops, t, table, sets[i % nsets], cos, sin)
-    torch.cuda.synchronize()
     k = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(k)]
+    ev_start = torch.cuda.Event(enable_timing=True)
+    ev_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev_start.record(stream)
     for i in range(k):
-        s = sets[i % nsets]
-        e = ev[i]
-        e[0].record(stream)
-        ops.embedding_hip(s["ids"], table)
-        e[1].record(stream)
-        qkv = s["qkv"]
-        ops.qk_norm_rope_hip(qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), s["qw"],
-                             s["kw"], 1e-6, cos, sin, s["pos"])
-        e[2].record(stream)
-        ops.fused_add_rmsnorm_hip(s["x"], s["r"], s["w"], 1e-6)
-        e[3].record(stream)
+        _run_chain(ops, t, table, sets[i % nsets], cos, sin)
+    ev_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    seg = [[ev[i][j].elapsed_time(ev[i][j + 1]) * 1e3 for i in range(k)] for j in range(3)]
-    step_us = [ev[i][0].elapsed_time(ev[i][3]) * 1e3 for i in range(k)]
     ms_per_step = wall * 1e3 / k
+    gpu_step_us = ev_start.elapsed_time(ev_end) * 1e3 / k
     chain_bytes = _chain_bytes(t)
-    gpu_step_us = statistics.mean(step_us)
     value = chain_bytes / (ms_per_step * 1e-3) / 1e9
+    del sets, table
+    torch.cuda.empty_cache()
 
-    add_bytes = 8 * t * 4096 + 4096 * 2
-    add_us = statistics.mean(seg[2])
+    # ---- roofline of the step's dominant kernel (add + RMSNorm, [8192, 4096] bf16) -------
+    # Timed live with hipEvents around back-to-back launches on the launch stream (events
+    # between the chain's kernels would add their own ~5 us each to the interval).
+    add_op = next(o for o in _ops(torch, ops, tables) if o.name == "add_rmsnorm" and o.config == "4c"
+                  and o.shape.startswith("[8192,"))
+    add_us, _ = _time_op(torch, add_op, 256)
+    add_bytes = add_op.nbytes
     achieved = add_bytes / (add_us * 1e-6) / 1e9
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("add_rmsnorm_T8192_bytes")
-        except (ValueError, OSError):
-            traffic = None
+    traffic = _profiled_traffic("add_rmsnorm_T8192_bytes")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
                 "kernel": "k_rmsnorm<bf16, RESID> (fused residual add + RMSNorm), [8192, 4096] bf16",
                 "bytes_per_launch": add_bytes, "avg_launch_us": round(add_us, 2)}
-    del sets, table
     torch.cuda.empty_cache()
 
     # ---- per-layer sums ------------------------------------------------------------------

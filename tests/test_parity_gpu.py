@@ -321,9 +321,11 @@ def test_qk_norm_rope_equals_unfused_hip_chain():
     ops.qk_norm_rope_hip(qa, ka, qw.to(DEV), kw.to(DEV), 1e-6, cos, sin, pos.to(DEV))
     qb = ops.rmsnorm_hip(b[:, :4096].reshape(n * hq, d), qw.to(DEV), 1e-6).view(n, hq, d)
     kb = ops.rmsnorm_hip(b[:, 4096:5120].reshape(n * hk, d), kw.to(DEV), 1e-6).view(n, hk, d)
+    yq, yk = qb.cpu(), kb.cpu()
     ops.rope_hip(qb, kb, cos, sin, pos.to(DEV))
-    assert_ulp(qa, qb, 2, "q")
-    assert_ulp(ka, kb, 2, "k")
+    c, s = cos.cpu()[pos][:, :d // 2], sin.cpu()[pos][:, :d // 2]
+    assert_rope_of_norm_close(qa, qb.cpu(), yq, c, s, 2, "q")
+    assert_rope_of_norm_close(ka, kb.cpu(), yk, c, s, 2, "k")
 
 
 # ---------------------------------------------------------------- MLA latent path
