@@ -136,8 +136,11 @@ def _ops(torch, ops, tables):
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
+    rope("7b", 8192)  # Qwen2.5-7B prefill at T = 8192 (per-layer sum below)
     for t in (1, 256, 8192):
         silu("3", t)
+    for t in (256, 8192):
+        add_norm("7b", t, 3584, bf)  # Qwen2.5-7B hidden size
     for t in (256, 8192):
         embedding("4a", t)
         qk("4b", t)
@@ -304,6 +307,7 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=256, help="launches per op in the per-op table")
     ap.add_argument("--quick", action="store_true", help="skip the per-op table and the CPU baseline")
     ap.add_argument("--max-sets", type=int, default=512, help="cap on rotated input sets per op (profiler runs)")
+    ap.add_argument("--configs", default=None, help="comma list of config labels to keep in the per-op rows")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="comma list of ops: run only their per-op rows (profiler runs)")
     args = ap.parse_args()
@@ -338,8 +342,11 @@ def main() -> int:
     per_op = []
     if not args.quick:
         only = set(args.only.split(",")) if args.only else None
+        cfgs = set(args.configs.split(",")) if args.configs else None
         for op in _ops(torch, ops, tables):
             if (only and op.name not in only) or (not only and op.config == "cal"):
+                continue
+            if cfgs and op.config not in cfgs:
                 continue
             _log(f"per-op: {op.name} cfg {op.config} {op.shape}")
             us, nsets = _time_op(torch, op, args.reps, max_sets=args.max_sets)
@@ -411,6 +418,13 @@ def main() -> int:
                  row("silu_and_mul", "extra", 8192)]
         if all(p is not None for p in parts):
             us_per_layer["qwen3_8b_full_elementwise_set_T8192"] = round(sum(parts), 2)
+        # Qwen2.5-7B decoder layer's elementwise ops: 2 x add+RMSNorm (hidden 3584), rope
+        # (28 q + 4 kv heads), silu_and_mul (I = 18944), as qwen2.py:140-159 runs them.
+        for tt, rope_cfg in ((256, "2"), (8192, "7b")):
+            parts = [row("add_rmsnorm", "7b", tt), row("add_rmsnorm", "7b", tt), row("rope", rope_cfg, tt),
+                     row("silu_and_mul", "3", tt)]
+            if all(p is not None for p in parts):
+                us_per_layer[f"qwen2.5_7b_layer_T{tt}"] = round(sum(parts), 2)
 
     cpu = None
     if not args.quick and not args.no_cpu:

@@ -44,8 +44,11 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
   const int nh = hq + hk;
   const int64_t off = static_cast<int64_t>(j) * VEC;
 
-  // The head rows are loaded before the position is checked, so their HBM latency overlaps
-  // the position -> c/s table chain instead of following it.
+  // Load order matters: vector loads retire in issue order (vmcnt), so the position is
+  // loaded first, then the head rows; the c/s table loads then wait only for the position
+  // while the head rows are still in flight, and nothing branches on the position before
+  // the head-row loads are issued.
+  const int64_t p = pos[tok];
   Pack<T, VEC> x1[G];
   Pack<T, VEC> x2[G];
   T* ptr[G];
@@ -56,42 +59,41 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
     x1[g] = load_stream<T, VEC>(ptr[g]);
     x2[g] = load_stream<T, VEC>(ptr[g] + half);
   }
-  const int64_t p = pos[tok];
   const bool bad = p < 0 || p >= trows;
   const int64_t pc = bad ? 0 : p;
   float c[VEC];
   float s[VEC];
   load_vals<float, VEC>(cos_t + pc * tstride + off, c);
   load_vals<float, VEC>(sin_t + pc * tstride + off, s);
-  // Norm weights: a lane's heads are all q or, past the q heads, mostly k; load the q
-  // weight packs and, only when some of its heads are k heads, the k weight packs.
+  // Norm weights (L2-resident), issued after the table loads. With one head per lane the
+  // head is either a q or a k head, so one weight is loaded; with G > 1 a lane's heads may
+  // straddle the q/k boundary and both are loaded.
   float wq1[VEC], wq2[VEC], wk1[VEC], wk2[VEC];
+  Pack<WT, VEC> wp1, wp2;  // G == 1: kept packed, widened at use (no early wait)
   if constexpr (NORM) {
-    const bool any_q = static_cast<int>(hg) * G < hq;
-    const bool any_k = static_cast<int>(hg) * G + G - 1 >= hq;
-    const WT* w0 = any_q ? qw : kw;
-    load_vals<WT, VEC>(w0 + off, wq1);
-    load_vals<WT, VEC>(w0 + half + off, wq2);
-    if (any_q && any_k) {
+    if constexpr (G == 1) {
+      const WT* w0 = static_cast<int>(hg) < hq ? qw : kw;
+      wp1 = load_pack<WT, VEC>(w0 + off);
+      wp2 = load_pack<WT, VEC>(w0 + half + off);
+    } else {
+      load_vals<WT, VEC>(qw + off, wq1);
+      load_vals<WT, VEC>(qw + half + off, wq2);
       load_vals<WT, VEC>(kw + off, wk1);
       load_vals<WT, VEC>(kw + half + off, wk2);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        wk1[e] = wq1[e];
-        wk2[e] = wq2[e];
-      }
     }
   }
+  // Keep every load above this point: without it the scheduler computes the sum of squares
+  // (which waits for the head rows) before issuing the table loads, serialising the two
+  // latencies.
+  __builtin_amdgcn_sched_barrier(0);
 
-  if (bad) {  // an out-of-range position leaves the token's rows untouched
-    if (j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
-    return;
-  }
+  // No branch depends on the position: a branch would let the compiler sink the head-row
+  // loads below it (re-serialising them after the position load). An out-of-range
+  // position instead stores the loaded rows back unchanged.
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int h = static_cast<int>(hg) * G + g;
-    if (h < nh) {  // uniform across the J lanes of the head
+    if (G == 1 || h < nh) {  // uniform across the J lanes; always true for G == 1
       float f1[VEC];
       float f2[VEC];
 #pragma unroll
@@ -108,21 +110,24 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
         const bool isq = h < hq;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          f1[e] = round_to<T>(round_to<T>(f1[e] * inv) * (isq ? wq1[e] : wk1[e]));
-          f2[e] = round_to<T>(round_to<T>(f2[e] * inv) * (isq ? wq2[e] : wk2[e]));
+          const float w1 = G == 1 ? to_f32(wp1.v[e]) : (isq ? wq1[e] : wk1[e]);
+          const float w2 = G == 1 ? to_f32(wp2.v[e]) : (isq ? wq2[e] : wk2[e]);
+          f1[e] = round_to<T>(round_to<T>(f1[e] * inv) * w1);
+          f2[e] = round_to<T>(round_to<T>(f2[e] * inv) * w2);
         }
       }
       Pack<T, VEC> o1;
       Pack<T, VEC> o2;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        o1.v[e] = from_f32<T>(f1[e] * c[e] - f2[e] * s[e]);
-        o2.v[e] = from_f32<T>(f2[e] * c[e] + f1[e] * s[e]);
+        o1.v[e] = bad ? x1[g].v[e] : from_f32<T>(f1[e] * c[e] - f2[e] * s[e]);
+        o2.v[e] = bad ? x2[g].v[e] : from_f32<T>(f2[e] * c[e] + f1[e] * s[e]);
       }
       store_stream<T, VEC>(ptr[g], o1);
       store_stream<T, VEC>(ptr[g] + half, o2);
     }
   }
+  if (bad && j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
 }
 
 // Any head_dim, any alignment: one wave per (token, head), scalar accesses, loops over the
@@ -263,114 +268,152 @@ int check_rope_args(const RopeArgs& a) {
 //
 // deepseek.py:124-133 with the rope permutation folded into the weights: per token,
 //   latent[:R] = rmsnorm(c, w), latent[R:R+Dr] = rope(k_pe), q_pe[h] = rope(q_pe[h]).
-// Work is split into independent wave tasks so each wave has one short dependency chain
-// (position -> c/s table) and the launch has twice as many waves in flight: per token, one
-// "latent" wave (the R-wide row as NVC packs per lane, a whole-wave DPP reduction, plus
-// the single key head's rope on its first J lanes) and ceil(H * J / 64) "query" waves (J
-// lanes per query head, 64 / J heads per wave).
+// Work is split into independent wave tasks over groups of TPW consecutive tokens: one
+// "latent" wave (per token: the R-wide row as NVC packs per lane and a whole-wave DPP
+// reduction, plus the key head's rope on the first J lanes) and ceil(H * J / 64) "query"
+// waves (J lanes per query head). A wave issues the loads of all its TPW tokens before any
+// arithmetic (the launcher uses TPW = 1; see launch_mla_vec).
 
-template <typename T, typename WT, int VEC, int J, int NVC>
+template <typename T, typename WT, int VEC, int J, int NVC, int TPW>
 __global__ void __launch_bounds__(256)
 k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
       int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
       const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
-      const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts, int tasks_per_tok,
+      const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts, int tasks_per_group,
       uint32_t* __restrict__ err) {
   const int64_t task = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int64_t tok = task / tasks_per_tok;  // uniform across the wave
-  const int sub = static_cast<int>(task - tok * tasks_per_tok);
-  if (tok >= ntok) return;
+  const int64_t group = task / tasks_per_group;  // uniform across the wave
+  const int sub = static_cast<int>(task - group * tasks_per_group);
+  const int64_t tok0 = group * TPW;
+  if (tok0 >= ntok) return;
   const int j = lane % J;
   const int64_t off = static_cast<int64_t>(j) * VEC;
+  int64_t toks[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) toks[u] = min(tok0 + u, ntok - 1);  // loads stay in range
 
   if (sub == 0) {
-    // Latent row: c packs, weights, and (lanes < J) the key head, all loaded before the
-    // position so the HBM latency overlaps the position -> table chain.
+    // Latent rows. Positions first (vector loads retire in issue order, so the table loads
+    // then wait only for them), then c packs, weights, the key head, then the tables.
     const int ncv = R / VEC;
-    Pack<T, VEC> cv[NVC];
-    float wv[NVC][VEC];
+    int64_t p[TPW];
 #pragma unroll
-    for (int i = 0; i < NVC; ++i) {
-      const int vi = min(lane + i * kWave, ncv - 1);
-      cv[i] = load_stream<T, VEC>(c + tok * cts + static_cast<int64_t>(vi) * VEC);
-      load_vals<WT, VEC>(w + static_cast<int64_t>(vi) * VEC, wv[i]);
+    for (int u = 0; u < TPW; ++u) p[u] = pos[toks[u]];
+    Pack<T, VEC> cv[TPW][NVC];
+    Pack<T, VEC> k1[TPW], k2[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+#pragma unroll
+      for (int i = 0; i < NVC; ++i) {
+        const int vi = min(lane + i * kWave, ncv - 1);
+        cv[u][i] = load_stream<T, VEC>(c + toks[u] * cts + static_cast<int64_t>(vi) * VEC);
+      }
+      k1[u] = load_pack<T, VEC>(kpe + toks[u] * kts + off);
+      k2[u] = load_pack<T, VEC>(kpe + toks[u] * kts + half + off);
     }
-    const Pack<T, VEC> k1 = load_pack<T, VEC>(kpe + tok * kts + off);
-    const Pack<T, VEC> k2 = load_pack<T, VEC>(kpe + tok * kts + half + off);
-    const int64_t p = pos[tok];
-    const bool bad = p < 0 || p >= trows;
-    const int64_t pc = bad ? 0 : p;
-    float cc[VEC], sn[VEC];
-    load_vals<float, VEC>(cos_t + pc * tstride + off, cc);
-    load_vals<float, VEC>(sin_t + pc * tstride + off, sn);
+    Pack<WT, VEC> wv[NVC];
+#pragma unroll
+    for (int i = 0; i < NVC; ++i) wv[i] = load_pack<WT, VEC>(w + static_cast<int64_t>(min(lane + i * kWave, ncv - 1)) * VEC);
+    bool bad[TPW];
+    float cc[TPW][VEC], sn[TPW][VEC];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      bad[u] = p[u] < 0 || p[u] >= trows;
+      const int64_t pc = bad[u] ? 0 : p[u];
+      load_vals<float, VEC>(cos_t + pc * tstride + off, cc[u]);
+      load_vals<float, VEC>(sin_t + pc * tstride + off, sn[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all loads issued before any arithmetic
 
-    float v[NVC][VEC];
-    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < NVC; ++i) {
-      const bool ok = lane + i * kWave < ncv;
+    for (int u = 0; u < TPW; ++u) {
+      const bool live = tok0 + u < ntok;  // uniform across the wave
+      float v[NVC][VEC];
+      float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float f = ok ? to_f32(cv[i].v[e]) : 0.f;
-        v[i][e] = f;
-        ss += f * f;
+      for (int i = 0; i < NVC; ++i) {
+        const bool ok = lane + i * kWave < ncv;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float f = ok ? to_f32(cv[u][i].v[e]) : 0.f;
+          v[i][e] = f;
+          ss += f * f;
+        }
       }
-    }
-    const float tot = group_sum<kWave>(ss);
-    const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
-    T* lrow = lat + tok * lts;
+      const float tot = group_sum<kWave>(ss);
+      const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+      T* lrow = lat + toks[u] * lts;
 #pragma unroll
-    for (int i = 0; i < NVC; ++i) {
-      const int vi = lane + i * kWave;
-      if (vi < ncv) {
-        Pack<T, VEC> o;
+      for (int i = 0; i < NVC; ++i) {
+        const int vi = lane + i * kWave;
+        if (live && vi < ncv) {
+          Pack<T, VEC> o;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * wv[i][e]);
-        store_stream<T, VEC>(lrow + static_cast<int64_t>(vi) * VEC, o);
+          for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * to_f32(wv[i].v[e]));
+          store_stream<T, VEC>(lrow + static_cast<int64_t>(vi) * VEC, o);
+        }
       }
-    }
-    if (lane < J) {
-      Pack<T, VEC> o1, o2;
+      if (live && lane < J) {
+        Pack<T, VEC> o1, o2;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float f1 = to_f32(k1.v[e]);
-        const float f2 = to_f32(k2.v[e]);
-        // an out-of-range position zeroes the latent key slot (q_pe is left untouched)
-        o1.v[e] = from_f32<T>(bad ? 0.f : f1 * cc[e] - f2 * sn[e]);
-        o2.v[e] = from_f32<T>(bad ? 0.f : f2 * cc[e] + f1 * sn[e]);
+        for (int e = 0; e < VEC; ++e) {
+          const float f1 = to_f32(k1[u].v[e]);
+          const float f2 = to_f32(k2[u].v[e]);
+          // an out-of-range position zeroes the latent key slot (q_pe is left untouched)
+          o1.v[e] = from_f32<T>(bad[u] ? 0.f : f1 * cc[u][e] - f2 * sn[u][e]);
+          o2.v[e] = from_f32<T>(bad[u] ? 0.f : f2 * cc[u][e] + f1 * sn[u][e]);
+        }
+        store_stream<T, VEC>(lrow + R + off, o1);
+        store_stream<T, VEC>(lrow + R + half + off, o2);
       }
-      store_stream<T, VEC>(lrow + R + off, o1);
-      store_stream<T, VEC>(lrow + R + half + off, o2);
-      if (bad && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+      if (live && bad[u] && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
     }
     return;
   }
 
-  // Query heads (64 / J per wave).
+  // Query heads (64 / J per wave), TPW tokens.
   constexpr int kHeadsPerWave = kWave / J;
   const int head = (sub - 1) * kHeadsPerWave + lane / J;
   if (head >= H) return;  // whole J-lane groups
-  T* ptr = qpe + tok * qts + static_cast<int64_t>(head) * qhs + off;
-  const Pack<T, VEC> a1 = load_stream<T, VEC>(ptr);
-  const Pack<T, VEC> a2 = load_stream<T, VEC>(ptr + half);
-  const int64_t p = pos[tok];
-  const bool bad = p < 0 || p >= trows;
-  const int64_t pc = bad ? 0 : p;
-  float cc[VEC], sn[VEC];
-  load_vals<float, VEC>(cos_t + pc * tstride + off, cc);
-  load_vals<float, VEC>(sin_t + pc * tstride + off, sn);
-  if (bad) return;  // q_pe untouched; the latent wave reports the error
-  Pack<T, VEC> o1, o2;
+  int64_t p[TPW];
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    const float f1 = to_f32(a1.v[e]);
-    const float f2 = to_f32(a2.v[e]);
-    o1.v[e] = from_f32<T>(f1 * cc[e] - f2 * sn[e]);
-    o2.v[e] = from_f32<T>(f2 * cc[e] + f1 * sn[e]);
+  for (int u = 0; u < TPW; ++u) p[u] = pos[toks[u]];
+  T* ptr[TPW];
+  Pack<T, VEC> a1[TPW], a2[TPW];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    ptr[u] = qpe + toks[u] * qts + static_cast<int64_t>(head) * qhs + off;
+    a1[u] = load_stream<T, VEC>(ptr[u]);
+    a2[u] = load_stream<T, VEC>(ptr[u] + half);
   }
-  store_stream<T, VEC>(ptr, o1);
-  store_stream<T, VEC>(ptr + half, o2);
+  bool bad[TPW];
+  float cc[TPW][VEC], sn[TPW][VEC];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    bad[u] = p[u] < 0 || p[u] >= trows;
+    const int64_t pc = bad[u] ? 0 : p[u];
+    load_vals<float, VEC>(cos_t + pc * tstride + off, cc[u]);
+    load_vals<float, VEC>(sin_t + pc * tstride + off, sn[u]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Branch-free as in k_rope: a bad position stores q_pe back unchanged (the latent wave
+  // reports the error).
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    Pack<T, VEC> o1, o2;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float f1 = to_f32(a1[u].v[e]);
+      const float f2 = to_f32(a2[u].v[e]);
+      o1.v[e] = bad[u] ? a1[u].v[e] : from_f32<T>(f1 * cc[u][e] - f2 * sn[u][e]);
+      o2.v[e] = bad[u] ? a2[u].v[e] : from_f32<T>(f2 * cc[u][e] + f1 * sn[u][e]);
+    }
+    if (tok0 + u < ntok) {
+      store_stream<T, VEC>(ptr[u], o1);
+      store_stream<T, VEC>(ptr[u] + half, o2);
+    }
+  }
 }
 
 // Any shape, any alignment: one wave per token, scalar accesses.
@@ -435,14 +478,17 @@ struct MlaArgs {
 
 template <typename T, typename WT, int VEC, int J, int NVC>
 int launch_mla_vec(const MlaArgs& a) {
-  const int64_t tasks_per_tok = 1 + cdiv(a.H * J, kWave);
-  const int64_t grid = cdiv(a.ntok * tasks_per_tok, 4);
+  // One token per wave task: measured on MI355X (Moonlight shape, T = 8192) TPW = 1, 2, 4
+  // take 14.8, 15.5 and 18.2 us. More waves in flight beat more bytes per wave here.
+  constexpr int TPW = 1;
+  const int64_t tasks_per_group = 1 + cdiv(a.H * J, kWave);
+  const int64_t grid = cdiv(cdiv(a.ntok, TPW) * tasks_per_group, 4);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC, TPW>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
                      static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
                      static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2),
                      static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
-                     static_cast<T*>(a.lat), a.lts, static_cast<int>(tasks_per_tok), a.err);
+                     static_cast<T*>(a.lat), a.lts, static_cast<int>(tasks_per_group), a.err);
   return launch_status();
 }
 
