@@ -21,6 +21,11 @@
 // packs once for all of them. The qk-norm sum of squares is a J-lane DPP reduction.
 #include "ember_common.h"
 
+#ifndef EMBER_ROPE_BLOCK
+#define EMBER_ROPE_BLOCK 256
+#endif
+constexpr int kRopeBlock = EMBER_ROPE_BLOCK;  // lanes per workgroup of k_rope and k_mla
+
 #ifndef EMBER_ROPE_G1_MAX_THREADS
 #define EMBER_ROPE_G1_MAX_THREADS (int64_t(1) << 26)
 #endif
@@ -29,13 +34,13 @@ namespace ember {
 namespace {
 
 template <typename T, typename WT, int VEC, int J, int G, bool NORM>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kRopeBlock)
 k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, int64_t kts, int64_t khs,
        int hk, int half, const WT* __restrict__ qw, const WT* __restrict__ kw, float eps,
        const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
        const int64_t* __restrict__ pos, uint32_t ntok, uint32_t ngroups, FastDiv gdiv,
        uint32_t* __restrict__ err) {
-  const uint32_t gt = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t gt = blockIdx.x * static_cast<uint32_t>(kRopeBlock) + threadIdx.x;
   const uint32_t j = gt % J;
   const uint32_t rowid = gt / J;
   const uint32_t tok = gdiv.div(rowid);
@@ -199,8 +204,8 @@ int launch_vec(const RopeArgs& a) {
   const int64_t ngroups = cdiv(nh, G);
   const int64_t threads = a.ntok * ngroups * J;
   if (threads > 0x7fffffffLL) return EMBER_EINVAL;  // FastDiv needs indices < 2^31
-  const int64_t grid = cdiv(threads, 256);
-  hipLaunchKernelGGL((k_rope<T, WT, VEC, J, G, NORM>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+  const int64_t grid = cdiv(threads, kRopeBlock);
+  hipLaunchKernelGGL((k_rope<T, WT, VEC, J, G, NORM>), dim3(static_cast<uint32_t>(grid)), dim3(kRopeBlock), 0, a.stream,
                      static_cast<T*>(a.q), a.qts, a.qhs, static_cast<int>(a.hq), static_cast<T*>(a.k), a.kts,
                      a.khs, static_cast<int>(a.hk), static_cast<int>(a.head_dim / 2),
                      static_cast<const WT*>(a.qw), static_cast<const WT*>(a.kw), a.eps, a.cos_t, a.sin_t,
@@ -275,13 +280,13 @@ int check_rope_args(const RopeArgs& a) {
 // arithmetic (the launcher uses TPW = 1; see launch_mla_vec).
 
 template <typename T, typename WT, int VEC, int J, int NVC, int TPW>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kRopeBlock)
 k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
       int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
       const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
       const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts, int tasks_per_group,
       uint32_t* __restrict__ err) {
-  const int64_t task = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int64_t task = static_cast<int64_t>(blockIdx.x) * (kRopeBlock / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int64_t group = task / tasks_per_group;  // uniform across the wave
   const int sub = static_cast<int>(task - group * tasks_per_group);
@@ -482,9 +487,9 @@ int launch_mla_vec(const MlaArgs& a) {
   // take 14.8, 15.5 and 18.2 us. More waves in flight beat more bytes per wave here.
   constexpr int TPW = 1;
   const int64_t tasks_per_group = 1 + cdiv(a.H * J, kWave);
-  const int64_t grid = cdiv(cdiv(a.ntok, TPW) * tasks_per_group, 4);
+  const int64_t grid = cdiv(cdiv(a.ntok, TPW) * tasks_per_group, kRopeBlock / kWave);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC, TPW>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
+  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC, TPW>), dim3(static_cast<uint32_t>(grid)), dim3(kRopeBlock), 0, a.stream,
                      static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
                      static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2),
                      static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,

@@ -87,6 +87,17 @@ class _on_device:
             torch.cuda.set_device(self.prev)
 
 
+def _require_device(what: str, *tensors: torch.Tensor) -> None:
+    """Every operand of a HIP launch must live on the same GPU: a host pointer or another
+    device's pointer handed to a kernel would fault the device, so it is refused here."""
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"{what}: tensors must be on a GPU, got {dev}")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"{what}: all tensors must be on {dev}, got one on {t.device}")
+
+
 def _rows2d(x: torch.Tensor) -> torch.Tensor:
     x2 = x.reshape(-1, x.shape[-1])
     if x2.shape[-1] > 1 and x2.stride(-1) != 1:
@@ -127,6 +138,7 @@ def _tables(cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor, d: in
 
 def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """ops_triton.py:90-97."""
+    _require_device("rmsnorm", x, weight)
     x2 = _rows2d(x)
     out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
     w, wtag = _weight_for(weight, x)
@@ -144,6 +156,7 @@ def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
 def fused_add_rmsnorm_hip(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
                           eps: float) -> tuple[torch.Tensor, torch.Tensor]:
     """ops_triton.py:100-110. Returns (normed, new_residual); the inputs are not modified."""
+    _require_device("fused_add_rmsnorm", x, residual, weight)
     if residual.dtype != x.dtype or residual.shape != x.shape:
         raise ValueError("x and residual must share shape and dtype")
     x2 = _rows2d(x)
@@ -167,6 +180,7 @@ def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
              positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """ops_triton.py:113-124: in place on q [N, H, D] and k [N, Hkv, D] (unit stride in D,
     any other strides); returns (q, k)."""
+    _require_device("rope", q, k, cos, sin, positions)
     n, h, d = q.shape
     hk = k.shape[1]
     if not (q.stride(2) == 1 and k.stride(2) == 1 and d % 2 == 0):
@@ -190,6 +204,7 @@ def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
 
 def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
     """ops_triton.py:127-134."""
+    _require_device("silu_and_mul", x)
     x2 = _rows2d(x)
     inter = x2.shape[-1] // 2
     out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)
@@ -206,6 +221,7 @@ def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
 
 def embedding_hip(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """nn.Embedding forward: out[..., :] = weight[ids[...], :], bit-exact."""
+    _require_device("embedding", weight, ids)
     if weight.dim() != 2:
         raise ValueError("embedding weight must be [vocab, hidden]")
     if ids.dtype not in (torch.int64, torch.int32):
@@ -235,6 +251,7 @@ def qk_norm_rope_hip(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
                      positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Qwen3 per-head RMSNorm of q and k, then neox rope, in place on the q/k views
     (qwen2.py:95-101 in one kernel); returns (q, k)."""
+    _require_device("qk_norm_rope", q, k, q_weight, k_weight, cos, sin, positions)
     n, h, d = q.shape
     hk = k.shape[1]
     if not (q.stride(2) == 1 and k.stride(2) == 1 and d % 2 == 0):
@@ -270,6 +287,7 @@ def mla_latent_rope_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor,
     latent c [N, R], rope of the single key head k_pe [N, Dr] (or [N, 1, Dr]) into a new
     latent [N, R + Dr], and rope of q_pe [N, H, Dr] in place. c and k_pe are not modified.
     Returns (q_pe, latent)."""
+    _require_device("mla_latent_rope", c, k_pe, q_pe, weight, cos, sin, positions)
     n, r = c.shape
     kp = k_pe.reshape(k_pe.shape[0], -1)
     nh, dr = q_pe.shape[1], q_pe.shape[2]

@@ -142,3 +142,27 @@ def test_layers_on_cpu():
     assert_bitexact(q.detach(), wq)
     assert_bitexact(k.detach(), wk)
     assert_bitexact(v, qkv[:, (hq + hk) * d:].view(n, hk, d))
+
+
+def test_hip_wrappers_refuse_host_tensors():
+    """A host pointer must never reach a kernel: every *_hip wrapper checks devices before
+    it loads the library or launches (runs without a GPU)."""
+    x = torch.randn(4, 64)
+    w = torch.ones(64)
+    cos, sin = ref.rope_tables(64, 16, 1e4)
+    pos = torch.arange(4)
+    q = x.view(4, 1, 64)
+    with pytest.raises(ValueError):
+        ops.rmsnorm_hip(x, w, 1e-6)
+    with pytest.raises(ValueError):
+        ops.fused_add_rmsnorm_hip(x, x, w, 1e-6)
+    with pytest.raises(ValueError):
+        ops.rope_hip(q, q, cos, sin, pos)
+    with pytest.raises(ValueError):
+        ops.silu_and_mul_hip(x)
+    with pytest.raises(ValueError):
+        ops.embedding_hip(pos, x)
+    with pytest.raises(ValueError):
+        ops.qk_norm_rope_hip(q, q, w, w, 1e-6, cos, sin, pos)
+    with pytest.raises(ValueError):
+        ops.mla_latent_rope_hip(x, x[:, :16], q[..., :16], w, 1e-6, cos, sin, pos)

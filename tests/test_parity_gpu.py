@@ -328,6 +328,56 @@ def test_qk_norm_rope_equals_unfused_hip_chain():
     assert_rope_of_norm_close(ka, kb.cpu(), yk, c, s, 2, "k")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_qk_norm_rope_fp32_weights(dtype):
+    """fp32 norm weights with half activations: y = round(fp32(round(x*inv) * w))."""
+    n, hq, hk, d = 24, 8, 2, 128
+    qkv, _, _, pos = gen.qkv_inputs(n, hq, hk, d, 4096, dtype, seed=70)
+    qw = _rand(d, dtype=torch.float32, seed=71, scale=0.1) + 1
+    kw = _rand(d, dtype=torch.float32, seed=72, scale=0.1) + 1
+    cos, sin = _tables(d, 4096, 1e6)
+    q = qkv[:, :hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    yq = ref.rmsnorm(q.reshape(n * hq, d), qw, 1e-6).to(dtype).view(n, hq, d)  # rounded as the kernel does
+    yk = ref.rmsnorm(k.reshape(n * hk, d), kw, 1e-6).to(dtype).view(n, hk, d)
+    want_q, want_k = ref.rope(yq, yk, cos, sin, pos)
+    qkv_d = qkv.to(DEV)
+    gq, gk = ops.qk_norm_rope_hip(qkv_d[:, :hq * d].view(n, hq, d), qkv_d[:, hq * d:(hq + hk) * d].view(n, hk, d),
+                                  qw.to(DEV), kw.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    c, s = cos[pos][:, :d // 2], sin[pos][:, :d // 2]
+    assert_rope_of_norm_close(gq, want_q, yq, c, s, 2, "q")
+    assert_rope_of_norm_close(gk, want_k, yk, c, s, 2, "k")
+
+
+def test_rope_and_qk_norm_without_k_heads():
+    """num_k_heads == 0 (a q-only rotation): the k pointer is never dereferenced."""
+    n, h, d = 16, 4, 128
+    q = _rand(n, h, d, dtype=torch.bfloat16, seed=73)
+    cos, sin = _tables(d, 256, 1e6)
+    pos = torch.randint(0, 256, (n,), generator=torch.Generator().manual_seed(74))
+    empty_k = torch.empty(n, 0, d, dtype=torch.bfloat16)
+    want_q, _ = ref.rope(q, empty_k, cos, sin, pos)
+    qd = q.to(DEV)
+    ops.rope_hip(qd, empty_k.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    assert_bitexact(qd, want_q, "q only")
+    w = _rand(d, dtype=torch.bfloat16, seed=75, scale=0.1) + 1
+    want_q, _ = ref.qk_norm_rope(q, empty_k, w, w, 1e-6, cos, sin, pos)
+    qd = q.to(DEV)
+    ops.qk_norm_rope_hip(qd, empty_k.to(DEV), w.to(DEV), w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    yq = ref.rmsnorm(q.reshape(n * h, d), w, 1e-6).view(n, h, d)
+    assert_rope_of_norm_close(qd, want_q, yq, cos[pos][:, :d // 2], sin[pos][:, :d // 2], 2, "q only, normed")
+
+
+def test_rmsnorm_on_strided_latent_view():
+    """kv_a_layernorm on the c view of the fused MLA projection (row stride 3648,
+    deepseek.py:126): no copy, same result as on a contiguous copy."""
+    buf = _rand(40, 3648, dtype=torch.bfloat16, seed=76)
+    w = _rand(512, dtype=torch.bfloat16, seed=77, scale=0.1) + 1
+    c = buf[:, 3072:3584]
+    got = ops.rmsnorm_hip(buf.to(DEV)[:, 3072:3584], w.to(DEV), 1e-6)
+    assert_ulp(got, ref.rmsnorm(c, w, 1e-6), 2, "strided c")
+
+
 # ---------------------------------------------------------------- MLA latent path
 
 def _mla_case(tokens, in_model, dtype=torch.bfloat16, seed=60, heads=16, nope=128, dr=64, rank=512):
@@ -375,6 +425,33 @@ def test_mla_latent_rope_config5(in_model, tokens):
     assert_bitexact(q_nope_d, q_nope, "q_nope untouched")
     assert_bitexact(c_d, c_before, "c unmodified")
     assert_bitexact(k_pe_d, kpe_before, "k_pe unmodified")
+
+
+def test_mla_fp32_weight():
+    kv_a, q, _, pos = gen.mla_inputs(30, 16, 128, 64, 512, 8192, torch.bfloat16, seed=78)
+    w = _rand(512, dtype=torch.float32, seed=79, scale=0.1) + 1
+    cos, sin = _tables(64, 8192, 5e4)
+    qv = q.view(30, 16, 192)
+    want_q_pe, want_lat = ref.mla_latent_rope(kv_a[:, :512], kv_a[:, 512:], qv[..., 128:], w, 1e-6, cos, sin, pos)
+    kd, qd = kv_a.to(DEV), q.to(DEV)
+    got_q_pe, lat = ops.mla_latent_rope_hip(kd[:, :512], kd[:, 512:], qd[..., 128:], w.to(DEV), 1e-6, cos.to(DEV),
+                                            sin.to(DEV), pos.to(DEV))
+    # fp32 weight: the oracle's product is fp32 (torch promotion); the kernel rounds it once
+    assert_ulp(lat[:, :512], want_lat[:, :512].to(torch.bfloat16), 2, "latent c, fp32 weight")
+    assert_bitexact(lat[:, 512:], want_lat[:, 512:].to(torch.bfloat16), "latent k_pe")
+    assert_bitexact(got_q_pe, want_q_pe, "q_pe")
+
+
+def test_mla_position_out_of_range(monkeypatch):
+    kv_a, q, w, pos = gen.mla_inputs(8, 4, 32, 64, 128, 64, torch.bfloat16, seed=80)
+    pos[5] = 64
+    cos, sin = _tables(64, 64, 1e4)
+    kd, qd = kv_a.to(DEV), q.to(DEV)
+    monkeypatch.setenv("EMBERSERVE_CHECK_INDICES", "1")
+    with pytest.raises(IndexError):
+        ops.mla_latent_rope_hip(kd[:, :128], kd[:, 128:], qd[..., 32:], w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV),
+                                pos.to(DEV))
+    assert_bitexact(qd[5], q[5], "bad token's q untouched")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
