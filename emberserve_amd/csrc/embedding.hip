@@ -69,7 +69,11 @@ k_embedding(const int64_t* __restrict__ ids, int64_t ntok, const uint8_t* __rest
             int64_t w_stride_bytes, uint8_t* __restrict__ out, int64_t out_stride_bytes, int nunits,
             uint32_t* __restrict__ err) {
   using V = typename Unit<VB>::type;
-  const int64_t tok = static_cast<int64_t>(blockIdx.x) * (256 / TPR) + threadIdx.x / TPR;
+  static_assert(TPR % kWave == 0, "a wave must not straddle two tokens");
+  // Wave-uniform token index (readfirstlane): the id is then a scalar load, and the row
+  // address an SGPR base.
+  const int64_t tok = __builtin_amdgcn_readfirstlane(
+      static_cast<int>(blockIdx.x * (256 / TPR) + threadIdx.x / TPR));
   const int lane = threadIdx.x % TPR;
   if (tok >= ntok) return;
   const int64_t id = ids[tok];
@@ -99,7 +103,7 @@ int launch_vb(const int64_t* ids, int64_t ntok, const void* w, int64_t vocab, in
   const int64_t nunits = row_bytes / VB;
   constexpr int kTpr = EMBER_EMB_TPR;
   const int64_t grid = cdiv(ntok, 256 / kTpr);
-  if (grid > 0x7fffffffLL || nunits > 0x7fffffffLL) return EMBER_EINVAL;
+  if (grid * 256 > 0x7fffffffLL || nunits > 0x7fffffffLL) return EMBER_EINVAL;
   hipLaunchKernelGGL((k_embedding<VB, EMBER_EMB_U, kTpr>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, stream, ids, ntok,
                      static_cast<const uint8_t*>(w), vocab, wsb, static_cast<uint8_t*>(out), osb,
                      static_cast<int>(nunits), err);

@@ -69,22 +69,19 @@ def _raise_index_errors() -> None:
         raise IndexError("emberserve_amd.rope: position out of range of the cos/sin table")
 
 
-class _on_device:
-    """Makes `t`'s GPU current for the duration of a launch (no-op when it already is)."""
-
-    def __init__(self, t: torch.Tensor) -> None:
-        self.idx = t.device.index
-        self.prev: int | None = None
-
-    def __enter__(self) -> None:
-        cur = torch.cuda.current_device()
-        if self.idx is not None and self.idx != cur:
-            self.prev = cur
-            torch.cuda.set_device(self.idx)
-
-    def __exit__(self, *exc) -> None:
-        if self.prev is not None:
-            torch.cuda.set_device(self.prev)
+def _launch(what: str, fn, device: torch.device, *args) -> None:
+    """Calls C-ABI entry point `fn(*args, stream)` with `device` current and torch's current
+    stream on it (the capture stream while a torch.cuda.graph records), raising on a
+    non-zero status. Uses torch's raw-handle accessors: this is on every op's hot path."""
+    idx = device.index
+    cur = torch._C._cuda_getDevice()
+    if idx is None or idx == cur:
+        st = fn(*args, torch._C._cuda_getCurrentRawStream(cur))
+    else:
+        with torch.cuda.device(idx):
+            st = fn(*args, torch._C._cuda_getCurrentRawStream(idx))
+    if st != 0:
+        _lib.check(st, what)
 
 
 def _require_device(what: str, *tensors: torch.Tensor) -> None:
@@ -144,12 +141,10 @@ def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
     w, wtag = _weight_for(weight, x)
     if w.numel() != x2.shape[1]:
         raise ValueError(f"weight has {w.numel()} elements, rows have {x2.shape[1]}")
-    lib = _lib.load()
-    with _on_device(x):
-        st = lib.ember_rmsnorm(x2.data_ptr(), x2.stride(0), w.data_ptr(), wtag, out.data_ptr(),
-                               out.stride(0), x2.shape[0], x2.shape[1], float(eps),
-                               _lib.dtype_tag(x.dtype), _lib.stream_handle(x.device))
-    _lib.check(st, "ember_rmsnorm")
+    _launch("ember_rmsnorm", _lib.load().ember_rmsnorm, x.device,
+            x2.data_ptr(), x2.stride(0), w.data_ptr(), wtag, out.data_ptr(),
+            out.stride(0), x2.shape[0], x2.shape[1], float(eps),
+            _lib.dtype_tag(x.dtype))
     return out.view(x.shape)
 
 
@@ -166,13 +161,10 @@ def fused_add_rmsnorm_hip(x: torch.Tensor, residual: torch.Tensor, weight: torch
     w, wtag = _weight_for(weight, x)
     if w.numel() != x2.shape[1]:
         raise ValueError(f"weight has {w.numel()} elements, rows have {x2.shape[1]}")
-    lib = _lib.load()
-    with _on_device(x):
-        st = lib.ember_fused_add_rmsnorm(
+    _launch("ember_fused_add_rmsnorm", _lib.load().ember_fused_add_rmsnorm, x.device,
             x2.data_ptr(), x2.stride(0), r2.data_ptr(), r2.stride(0), w.data_ptr(), wtag,
             out.data_ptr(), out.stride(0), new_res.data_ptr(), new_res.stride(0), x2.shape[0],
-            x2.shape[1], float(eps), _lib.dtype_tag(x.dtype), _lib.stream_handle(x.device))
-    _lib.check(st, "ember_fused_add_rmsnorm")
+            x2.shape[1], float(eps), _lib.dtype_tag(x.dtype))
     return out.view(x.shape), new_res.view(residual.shape)
 
 
@@ -190,13 +182,10 @@ def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
     if n == 0:
         return q, k
     cos, sin, positions = _tables(cos, sin, positions, d)
-    lib = _lib.load()
-    with _on_device(q):
-        st = lib.ember_rope(q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
-                            k.stride(1), hk, d, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
-                            cos.stride(0), positions.data_ptr(), n, _lib.dtype_tag(q.dtype),
-                            _lib.stream_handle(q.device))
-    _lib.check(st, "ember_rope")
+    _launch("ember_rope", _lib.load().ember_rope, q.device,
+            q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
+            k.stride(1), hk, d, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+            cos.stride(0), positions.data_ptr(), n, _lib.dtype_tag(q.dtype))
     if _check_indices():
         _raise_index_errors()
     return q, k
@@ -210,12 +199,9 @@ def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)
     if inter == 0 or x2.shape[0] == 0:
         return out.view(*x.shape[:-1], inter)
-    lib = _lib.load()
-    with _on_device(x):
-        st = lib.ember_silu_and_mul(x2.data_ptr(), x2.stride(0), out.data_ptr(), out.stride(0),
-                                    x2.shape[0], inter, _lib.dtype_tag(x.dtype),
-                                    _lib.stream_handle(x.device))
-    _lib.check(st, "ember_silu_and_mul")
+    _launch("ember_silu_and_mul", _lib.load().ember_silu_and_mul, x.device,
+            x2.data_ptr(), x2.stride(0), out.data_ptr(), out.stride(0),
+            x2.shape[0], inter, _lib.dtype_tag(x.dtype))
     return out.view(*x.shape[:-1], inter)
 
 
@@ -235,12 +221,9 @@ def embedding_hip(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     out = torch.empty((flat.shape[0], w.shape[1]), dtype=w.dtype, device=w.device)
     if flat.shape[0] == 0:
         return out.view(*ids.shape, w.shape[1])
-    lib = _lib.load()
-    with _on_device(w):
-        st = lib.ember_embedding(flat.data_ptr(), flat.shape[0], w.data_ptr(), w.shape[0], w.shape[1],
-                                 w.stride(0), out.data_ptr(), out.stride(0), w.element_size(),
-                                 _lib.stream_handle(w.device))
-    _lib.check(st, "ember_embedding")
+    _launch("ember_embedding", _lib.load().ember_embedding, w.device,
+            flat.data_ptr(), flat.shape[0], w.data_ptr(), w.shape[0], w.shape[1],
+            w.stride(0), out.data_ptr(), out.stride(0), w.element_size())
     if _check_indices():
         _raise_index_errors()
     return out.view(*ids.shape, w.shape[1])
@@ -267,14 +250,11 @@ def qk_norm_rope_hip(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
     if qtag != ktag:
         qw, kw, qtag = qw.float(), kw.float(), _lib.F32
     cos, sin, positions = _tables(cos, sin, positions, d)
-    lib = _lib.load()
-    with _on_device(q):
-        st = lib.ember_qk_norm_rope(q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
-                                    k.stride(1), hk, d, qw.data_ptr(), kw.data_ptr(), qtag, float(eps),
-                                    cos.data_ptr(), sin.data_ptr(), cos.shape[0], cos.stride(0),
-                                    positions.data_ptr(), n, _lib.dtype_tag(q.dtype),
-                                    _lib.stream_handle(q.device))
-    _lib.check(st, "ember_qk_norm_rope")
+    _launch("ember_qk_norm_rope", _lib.load().ember_qk_norm_rope, q.device,
+            q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0),
+            k.stride(1), hk, d, qw.data_ptr(), kw.data_ptr(), qtag, float(eps),
+            cos.data_ptr(), sin.data_ptr(), cos.shape[0], cos.stride(0),
+            positions.data_ptr(), n, _lib.dtype_tag(q.dtype))
     if _check_indices():
         _raise_index_errors()
     return q, k
@@ -304,14 +284,11 @@ def mla_latent_rope_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor,
         return q_pe, latent
     w, wtag = _weight_for(weight, c)
     cos, sin, positions = _tables(cos, sin, positions, dr)
-    lib = _lib.load()
-    with _on_device(c):
-        st = lib.ember_mla_latent_rope(
+    _launch("ember_mla_latent_rope", _lib.load().ember_mla_latent_rope, c.device,
             c.data_ptr(), c.stride(0), r, kp.data_ptr(), kp.stride(0), q_pe.data_ptr(), q_pe.stride(0),
             q_pe.stride(1), nh, dr, w.data_ptr(), wtag, float(eps), cos.data_ptr(), sin.data_ptr(),
             cos.shape[0], cos.stride(0), positions.data_ptr(), n, latent.data_ptr(), latent.stride(0),
-            _lib.dtype_tag(c.dtype), _lib.stream_handle(c.device))
-    _lib.check(st, "ember_mla_latent_rope")
+            _lib.dtype_tag(c.dtype))
     if _check_indices():
         _raise_index_errors()
     return q_pe, latent
