@@ -15,7 +15,8 @@ Also printed in the same JSON line:
   roofline      the dominant kernel of the step (add+RMSNorm, T=8192), timed live with
                 hipEvents around back-to-back launches on its launch stream
   cpu_baseline  the CPU oracle (the reference's PyTorch-eager ops restated) on a bounded
-                sample of the same chain on this host
+                sample of the same chain on this host; every per-op row also carries the
+                oracle's CPU time on the same shape (cpu_us, cpu_GB/s)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--only OP]
 """
@@ -44,11 +45,76 @@ def _log(msg: str) -> None:
 # ----------------------------------------------------------------------------- workloads
 
 class Op:
-    """A benchmarked launch: `make(i)` builds input set i on the GPU, `run(args)` launches."""
+    """A benchmarked launch: `make(i)` builds input set i on the GPU, `run(args)` launches.
+    `cpu()` (optional) returns a zero-argument callable running the CPU oracle on the same
+    shape (seeded inputs from oracle/inputs.py), for the per-row CPU timing."""
 
-    def __init__(self, name, config, shape, nbytes, make, run, footprint):
+    def __init__(self, name, config, shape, nbytes, make, run, footprint, cpu=None):
         self.name, self.config, self.shape, self.nbytes = name, config, shape, nbytes
-        self.make, self.run, self.footprint = make, run, footprint
+        self.make, self.run, self.footprint, self.cpu = make, run, footprint, cpu
+
+
+_CPU_CACHE = {}
+
+
+def _cpu_inputs(key, build):
+    """CPU oracle inputs, built once per key (the 1.24 GB embedding table above all)."""
+    if key not in _CPU_CACHE:
+        _CPU_CACHE[key] = build()
+    return _CPU_CACHE[key]
+
+
+def _cpu_factories():
+    """name -> factory(params) -> zero-arg CPU callable, using the oracle (test infrastructure,
+    imported here only for the CPU baseline)."""
+    import torch
+
+    from oracle import inputs as gen
+    from oracle import ref_ops as ref
+
+    def add_norm(t, h, dtype):
+        x, r, w = _cpu_inputs(("add", t, h, dtype), lambda: gen.add_rmsnorm_inputs(t, h, dtype))
+        return lambda: ref.fused_add_rmsnorm(x, r, w, 1e-6)
+
+    def rope(t):
+        q, k, pos = _cpu_inputs(("rope", t), lambda: gen.rope_inputs(t, 28, 4, 128, 32768, torch.bfloat16))
+        cos, sin = _cpu_inputs(("tab", 128, 32768, 1e6), lambda: ref.rope_tables(128, 32768, 1e6))
+        return lambda: ref.rope(q, k, cos, sin, pos)
+
+    def silu(t, inter, dtype):
+        x = _cpu_inputs(("silu", t, inter, dtype), lambda: gen.silu_inputs(t, inter, dtype))
+        return lambda: ref.silu_and_mul(x)
+
+    def embedding(t):
+        _, w = _cpu_inputs(("emb_table",), lambda: gen.embedding_inputs(1, 151936, 4096, torch.bfloat16, seed=1))
+        ids = gen.uniform_ints(t, 151936, 7)
+        return lambda: ref.embedding(ids, w)
+
+    def qk(t):
+        qkv, qw, kw, pos = _cpu_inputs(("qkv", t), lambda: gen.qkv_inputs(t, 32, 8, 128, 40960, torch.bfloat16))
+        cos, sin = _cpu_inputs(("tab", 128, 40960, 1e6), lambda: ref.rope_tables(128, 40960, 1e6))
+        q, k = qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128)
+        return lambda: ref.qk_norm_rope(q, k, qw, kw, 1e-6, cos, sin, pos)
+
+    def mla(t):
+        kv_a, q, w, pos = _cpu_inputs(("mla", t), lambda: gen.mla_inputs(t, 16, 128, 64, 512, 8192, torch.bfloat16))
+        cos, sin = _cpu_inputs(("tab", 64, 8192, 5e4), lambda: ref.rope_tables(64, 8192, 5e4))
+        qv = q.view(t, 16, 192)
+        return lambda: ref.mla_latent_rope(kv_a[:, :512], kv_a[:, 512:], qv[..., 128:], w, 1e-6, cos, sin, pos)
+
+    return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla)
+
+
+def _cpu_time_row(fn, budget_s):
+    """Median seconds of the CPU oracle call: 1 warm-up, then up to 3 reps within budget."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
 
 
 def _ops(torch, ops, tables):
@@ -72,7 +138,8 @@ def _ops(torch, ops, tables):
                     randn((h,), dtype, 3 * i + 2, 1.0, 0.1))
         nbytes = 4 * t * h * 2 + h * 2
         out.append(Op("add_rmsnorm", cfg, f"[{t},{h}] {str(dtype)[6:]}", nbytes, make,
-                      lambda a: ops.fused_add_rmsnorm_hip(a[0], a[1], a[2], 1e-6), 4 * t * h * 2))
+                      lambda a: ops.fused_add_rmsnorm_hip(a[0], a[1], a[2], 1e-6), 4 * t * h * 2,
+                      cpu=("add_norm", (t, h, dtype))))
 
     def rope(cfg, t):
         cos, sin = tables(128, 32768, 1e6)
@@ -82,14 +149,14 @@ def _ops(torch, ops, tables):
                     randint(t, 32768, 3 * i + 2))
         nbytes = 2 * t * 32 * 128 * 2 + 8 * t
         out.append(Op("rope", cfg, f"q[{t},28,128] k[{t},4,128] bf16", nbytes, make,
-                      lambda a: ops.rope_hip(a[0], a[1], cos, sin, a[2]), nbytes))
+                      lambda a: ops.rope_hip(a[0], a[1], cos, sin, a[2]), nbytes, cpu=("rope", (t,))))
 
     def silu(cfg, t, inter=18944, dtype=f16, label="silu_and_mul"):
         def make(i):
             return (randn((t, 2 * inter), dtype, i, 0.0, 2.0),)
         nbytes = 3 * t * inter * 2
         out.append(Op(label, cfg, f"[{t},{2 * inter}] {str(dtype)[6:]}", nbytes, make,
-                      lambda a: ops.silu_and_mul_hip(a[0]), nbytes))
+                      lambda a: ops.silu_and_mul_hip(a[0]), nbytes, cpu=("silu", (t, inter, dtype))))
 
     table_cache = {}
 
@@ -100,7 +167,7 @@ def _ops(torch, ops, tables):
             return (randint(t, 151936, i), table_cache["w"])
         nbytes = t * (8 + 2 * 4096 * 2)
         out.append(Op("embedding", cfg, f"table[151936,4096] bf16, T={t}", nbytes, make,
-                      lambda a: ops.embedding_hip(a[0], a[1]), nbytes))
+                      lambda a: ops.embedding_hip(a[0], a[1]), nbytes, cpu=("embedding", (t,))))
 
     def qk(cfg, t):
         cos, sin = tables(128, 40960, 1e6)
@@ -113,7 +180,7 @@ def _ops(torch, ops, tables):
         nbytes = 2 * t * 40 * 128 * 2 + 8 * t + 2 * 128 * 2
         out.append(Op("qk_norm_rope", cfg, f"qkv[{t},6144] 32q+8kv x128 bf16", nbytes, make,
                       lambda a: ops.qk_norm_rope_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4]),
-                      t * 6144 * 2))
+                      t * 6144 * 2, cpu=("qk", (t,))))
 
     def mla(cfg, t, in_model):
         cos, sin = tables(64, 8192, 5e4)
@@ -131,7 +198,7 @@ def _ops(torch, ops, tables):
         layout = "views of one [T,3648] row" if in_model else "separate tensors"
         out.append(Op("mla_latent_rope", cfg, f"kv_a[{t},576] q[{t},16,192] bf16 ({layout})", nbytes, make,
                       lambda a: ops.mla_latent_rope_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4]),
-                      t * (576 + 3072 + 576) * 2))
+                      t * (576 + 3072 + 576) * 2, cpu=("mla", (t,)) if not in_model else None))
 
     add_norm("1", 256, 896, f16)
     rope("2", 256)
@@ -256,7 +323,8 @@ def _cpu_baseline(t, budget_s):
 
     cores = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(cores)
-    ids, table = gen.embedding_inputs(t, 151936, 4096, torch.bfloat16, seed=1)
+    _, table = _cpu_inputs(("emb_table",), lambda: gen.embedding_inputs(1, 151936, 4096, torch.bfloat16, seed=1))
+    ids = gen.uniform_ints(t, 151936, 2)
     qkv, qw, kw, pos = gen.qkv_inputs(t, 32, 8, 128, 40960, torch.bfloat16, seed=2)
     x, r, w = gen.add_rmsnorm_inputs(t, 4096, torch.bfloat16, seed=3)
     cos, sin = ref.rope_tables(128, 40960, 1e6)
@@ -279,6 +347,16 @@ def _cpu_baseline(t, budget_s):
             "kind": "port", "ms_per_step": round(sec * 1e3, 2),
             "sample": f"Qwen3-8B chain (embedding + qk-norm/rope + add+RMSNorm) at T={t}, "
                       f"median of {len(times)} reps after 1 warm-up, torch {torch.__version__} CPU eager"}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _profiled_traffic(key):
@@ -340,6 +418,7 @@ def main() -> int:
 
     result = {}
     per_op = []
+    cpu_rows = []
     if not args.quick:
         only = set(args.only.split(",")) if args.only else None
         cfgs = set(args.configs.split(",")) if args.configs else None
@@ -354,6 +433,7 @@ def main() -> int:
             per_op.append({"op": op.name, "config": op.config, "shape": op.shape, "bytes": op.nbytes,
                            "us": round(us, 2), "GB/s": round(gbps, 1),
                            "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "input_sets": nsets})
+            cpu_rows.append((op, per_op[-1]))
             torch.cuda.empty_cache()
         if args.only:
             print(json.dumps({"per_op": per_op}))
@@ -430,6 +510,18 @@ def main() -> int:
     if not args.quick and not args.no_cpu:
         _log("cpu baseline")
         cpu = _cpu_baseline(8192, budget_s=20.0)
+        cpu["cpu_model"] = _cpu_model()
+        # The same oracle on every per-op row (bounded: one warm-up, up to 3 reps in ~1 s).
+        facts = _cpu_factories()
+        for op, row in cpu_rows:
+            if op.cpu is None:
+                continue
+            _log(f"cpu row: {op.name} cfg {op.config} {op.shape}")
+            kind, params = op.cpu
+            sec, reps = _cpu_time_row(facts[kind](*params), budget_s=1.0)
+            row["cpu_us"] = round(sec * 1e6, 1)
+            row["cpu_GB/s"] = round(op.nbytes / sec / 1e9, 3)
+        _CPU_CACHE.clear()
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": k,
