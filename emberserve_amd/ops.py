@@ -194,6 +194,8 @@ def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
 def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
     """ops_triton.py:127-134."""
     _require_device("silu_and_mul", x)
+    if x.shape[-1] % 2 != 0:  # the eager form fails the same way: halves of unequal size
+        raise ValueError(f"silu_and_mul: last dim {x.shape[-1]} is not even")
     x2 = _rows2d(x)
     inter = x2.shape[-1] // 2
     out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)

@@ -166,3 +166,11 @@ def test_hip_wrappers_refuse_host_tensors():
         ops.qk_norm_rope_hip(q, q, w, w, 1e-6, cos, sin, pos)
     with pytest.raises(ValueError):
         ops.mla_latent_rope_hip(x, x[:, :16], q[..., :16], w, 1e-6, cos, sin, pos)
+
+
+def test_silu_and_mul_rejects_odd_width():
+    with pytest.raises(RuntimeError):  # torch eager: the two halves differ in size
+        ops.silu_and_mul(torch.randn(2, 7))
+    if torch.cuda.is_available():
+        with pytest.raises(ValueError):
+            ops.silu_and_mul_hip(torch.randn(2, 7, device="cuda"))
