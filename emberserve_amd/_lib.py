@@ -13,11 +13,12 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
 ERR_ROPE_POS = 2
+ERR_KV_SLOT = 4
 
 _DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -40,6 +41,9 @@ SIGNATURES: dict[str, list] = {
                            _p, _p, _i64, _i64, _p, _i64, _i32, _p],
     "ember_mla_latent_rope": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _f32,
                               _p, _p, _i64, _i64, _p, _i64, _p, _i64, _i32, _p],
+    "ember_kv_cache_write": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _i64, _i64,
+                             _i64, _p],
+    "ember_latent_cache_write": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],

@@ -76,3 +76,19 @@ def mla_latent_rope_torch(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tenso
     kp = k_pe.reshape(k_pe.shape[0], 1, -1)
     q_rot, k_rot = rope_torch(q_pe, kp, cos, sin, positions)
     return q_rot, torch.cat([cn, k_rot.squeeze(1)], dim=-1)
+
+
+def kv_cache_write_torch(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """emberserve/kv/cache.py:54-61 for one layer: index_copy_ of k and v into the flat
+    [num_slots, Hkv, D] views of the caches."""
+    slots = slot_mapping.to(device=k_cache.device, dtype=torch.long)
+    flat = (-1, k.shape[1], k.shape[2])
+    k_cache.view(flat).index_copy_(0, slots, k.to(k_cache.dtype))
+    v_cache.view(flat).index_copy_(0, slots, v.to(v_cache.dtype))
+
+
+def latent_cache_write_torch(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
+    """emberserve/kv/cache.py:152-157 for one layer."""
+    slots = slot_mapping.to(device=cache.device, dtype=torch.long)
+    cache.view(-1, latent.shape[-1]).index_copy_(0, slots, latent.to(cache.dtype))

@@ -35,6 +35,8 @@ from .eager import (  # noqa: F401  (re-exported: the reference's names)
     _rotate_half,
     embedding_torch,
     fused_add_rmsnorm_torch,
+    kv_cache_write_torch,
+    latent_cache_write_torch,
     mla_latent_rope_torch,
     qk_norm_rope_torch,
     rmsnorm_torch,
@@ -48,6 +50,8 @@ __all__ = [
     "silu_and_mul_hip", "embedding_hip", "qk_norm_rope_hip", "mla_latent_rope_hip",
     "rmsnorm_torch", "fused_add_rmsnorm_torch", "rope_torch", "silu_and_mul_torch",
     "embedding_torch", "qk_norm_rope_torch", "mla_latent_rope_torch",
+    "kv_cache_write", "latent_cache_write", "kv_cache_write_hip", "latent_cache_write_hip",
+    "kv_cache_write_torch", "latent_cache_write_torch",
 ]
 
 
@@ -67,6 +71,8 @@ def _raise_index_errors() -> None:
         raise IndexError("emberserve_amd.embedding: token id out of range")
     if flags & _lib.ERR_ROPE_POS:
         raise IndexError("emberserve_amd.rope: position out of range of the cos/sin table")
+    if flags & _lib.ERR_KV_SLOT:
+        raise IndexError("emberserve_amd.kv_cache_write: slot out of range of the cache")
 
 
 def _launch(what: str, fn, device: torch.device, *args) -> None:
@@ -296,6 +302,59 @@ def mla_latent_rope_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor,
     return q_pe, latent
 
 
+def kv_cache_write_hip(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """PagedKVCache.write (kv/cache.py:54-61) for one layer: k, v [N, Hkv, D] (any token
+    and head strides, unit stride in D) scattered into k_cache / v_cache
+    [num_blocks, block_size, Hkv, D] (or already flat [num_slots, Hkv, D]) at slot_mapping
+    [N]. Bit-exact."""
+    _require_device("kv_cache_write", k, v, slot_mapping, k_cache, v_cache)
+    n, hk, d = k.shape
+    if v.shape != k.shape or k.dtype != v.dtype or k_cache.dtype != k.dtype or v_cache.dtype != k.dtype:
+        raise ValueError("kv_cache_write: k, v and the caches must agree in shape and dtype")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("kv_cache_write: k_cache and v_cache must share a geometry")
+    if tuple(k_cache.shape[-2:]) != (hk, d):
+        raise ValueError(f"kv_cache_write: cache rows are {tuple(k_cache.shape[-2:])}, k rows ({hk}, {d})")
+    if k.stride(2) != 1 or v.stride(2) != 1 or k_cache.stride(-1) != 1:
+        raise AssertionError("kv_cache_write: unit stride in head_dim required")
+    kc = k_cache.view(-1, hk, d)  # [num_slots, Hkv, D]; a view, so the write lands in the cache
+    if slot_mapping.numel() != n:
+        raise ValueError("kv_cache_write: one slot per token expected")
+    slots = slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.long()
+    slots = slots.contiguous()
+    if n == 0:
+        return
+    _launch("ember_kv_cache_write", _lib.load().ember_kv_cache_write, k.device,
+            k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), hk, d,
+            slots.data_ptr(), n, k_cache.data_ptr(), v_cache.data_ptr(), kc.shape[0], kc.stride(0),
+            kc.stride(1), k.element_size())
+    if _check_indices():
+        _raise_index_errors()
+
+
+def latent_cache_write_hip(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
+    """PagedLatentCache.write (kv/cache.py:152-157) for one layer: latent [N, L] rows
+    scattered into cache [num_blocks, block_size, L] at slot_mapping [N]. Bit-exact."""
+    _require_device("latent_cache_write", latent, slot_mapping, cache)
+    n, dim = latent.shape
+    if cache.dtype != latent.dtype or cache.shape[-1] != dim:
+        raise ValueError("latent_cache_write: cache rows must match the latent rows")
+    if latent.stride(1) != 1 or cache.stride(-1) != 1:
+        raise AssertionError("latent_cache_write: unit innermost stride required")
+    flat = cache.view(-1, dim)
+    if slot_mapping.numel() != n:
+        raise ValueError("latent_cache_write: one slot per token expected")
+    slots = (slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.long()).contiguous()
+    if n == 0:
+        return
+    _launch("ember_latent_cache_write", _lib.load().ember_latent_cache_write, latent.device,
+            latent.data_ptr(), latent.stride(0), dim, slots.data_ptr(), n, flat.data_ptr(), flat.shape[0],
+            flat.stride(0), latent.element_size())
+    if _check_indices():
+        _raise_index_errors()
+
+
 # ---- dispatch (ops.py:92-115 plus the fused additions) ----------------------------------
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -344,3 +403,16 @@ def mla_latent_rope(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, wei
     if fused_enabled(c):
         return mla_latent_rope_hip(c, k_pe, q_pe, weight, eps, cos, sin, positions)
     return mla_latent_rope_torch(c, k_pe, q_pe, weight, eps, cos, sin, positions)
+
+
+def kv_cache_write(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                   k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    if fused_enabled(k):
+        return kv_cache_write_hip(k, v, slot_mapping, k_cache, v_cache)
+    return kv_cache_write_torch(k, v, slot_mapping, k_cache, v_cache)
+
+
+def latent_cache_write(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
+    if fused_enabled(latent):
+        return latent_cache_write_hip(latent, slot_mapping, cache)
+    return latent_cache_write_torch(latent, slot_mapping, cache)

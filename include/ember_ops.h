@@ -13,10 +13,11 @@
  * detected on the host before any launch; a failed launch returns EMBER_ELAUNCH.
  * ember_status_string() names a code.
  *
- * Index safety: positions and token ids are checked on the device. An out-of-range
- * position leaves that token's rows untouched, an out-of-range id writes a zero row; both
- * set a bit in a per-device error word that ember_read_errors() returns (and optionally
- * clears). Reading it synchronises, so callers read it only in debug paths.
+ * Index safety: positions, token ids and cache slots are checked on the device. An
+ * out-of-range position leaves that token's rows untouched, an out-of-range id writes a
+ * zero row, an out-of-range slot skips the token; each sets a bit in a per-device error
+ * word that ember_read_errors() returns (and optionally clears). Reading it synchronises,
+ * so callers read it only in debug paths.
  *
  * Reference interfaces replaced (paths relative to the emberserve repository):
  *   ember_rmsnorm             emberserve/model/ops.py:92-95  (rmsnorm) and
@@ -33,6 +34,8 @@
  *                             emberserve/model/qwen2.py:95-101 (two rmsnorm + one rope)
  *   ember_mla_latent_rope     the kv_a_layernorm + rotary_emb + cat sequence of
  *                             emberserve/model/deepseek.py:124-133
+ *   ember_kv_cache_write      PagedKVCache.write, emberserve/kv/cache.py:54-61
+ *   ember_latent_cache_write  PagedLatentCache.write, emberserve/kv/cache.py:152-157
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
@@ -58,8 +61,9 @@ extern "C" {
 /* bits of the device error word */
 #define EMBER_ERR_EMBED_ID 1u   /* a token id outside [0, vocab) */
 #define EMBER_ERR_ROPE_POS 2u   /* a position outside [0, table_rows) */
+#define EMBER_ERR_KV_SLOT 4u    /* a cache slot outside [0, num_slots) */
 
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped when an entry point is added or its signature changes. */
 int ember_abi_version(void);
 
 /* Static description of a status code. */
@@ -150,6 +154,30 @@ int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora
                           int64_t table_rows, int64_t table_row_stride,
                           const int64_t* positions, int64_t num_tokens,
                           void* latent, int64_t latent_token_stride, int dtype, void* stream);
+
+/* Paged KV-cache write (PagedKVCache.write, kv/cache.py:54-61, an index_copy_ per tensor):
+ *   k_cache[slot_mapping[t], h, :] = k[t, h, :]
+ *   v_cache[slot_mapping[t], h, :] = v[t, h, :]        t < num_tokens, h < num_kv_heads
+ * Bit-exact copies of head_dim elements of elem_bytes bytes. Strides are in elements; the
+ * caches are [num_slots, ...] with slot stride cache_slot_stride and head stride
+ * cache_head_stride (both caches share the geometry). A slot outside [0, num_slots) skips
+ * that token and sets EMBER_ERR_KV_SLOT; with duplicate slots one writer wins, as with
+ * index_copy_. */
+int ember_kv_cache_write(const void* k, int64_t k_token_stride, int64_t k_head_stride,
+                         const void* v, int64_t v_token_stride, int64_t v_head_stride,
+                         int64_t num_kv_heads, int64_t head_dim,
+                         const int64_t* slot_mapping, int64_t num_tokens,
+                         void* k_cache, void* v_cache, int64_t num_slots,
+                         int64_t cache_slot_stride, int64_t cache_head_stride,
+                         int64_t elem_bytes, void* stream);
+
+/* Paged latent-cache write (PagedLatentCache.write, kv/cache.py:152-157):
+ *   cache[slot_mapping[t], :latent_dim] = latent[t, :latent_dim]
+ * Same slot rules as ember_kv_cache_write. */
+int ember_latent_cache_write(const void* latent, int64_t latent_token_stride, int64_t latent_dim,
+                             const int64_t* slot_mapping, int64_t num_tokens,
+                             void* cache, int64_t num_slots, int64_t cache_slot_stride,
+                             int64_t elem_bytes, void* stream);
 
 #ifdef __cplusplus
 }

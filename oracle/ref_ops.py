@@ -21,6 +21,8 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
   embedding                    numpy.take, bit-exact.
   qk_norm_rope, mla_latent_rope  float64 normalise-then-rotate closed forms; untouched
                                columns bit-exact.
+  kv_cache_write, latent_cache_write  an explicit per-token loop of slice assignments
+                               (slot by slot), bit-exact; untouched slots stay untouched.
 No function is left unpinned.
 """
 
@@ -129,3 +131,20 @@ def mla_latent_rope(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, wei
     q_pe, k_pe = rope(q_pe, k_pe.reshape(k_pe.shape[0], -1).unsqueeze(1), cos, sin, positions)
     latent = torch.cat([c, k_pe.squeeze(1)], dim=-1)
     return q_pe, latent
+
+
+def kv_cache_write(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+                   k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """emberserve/kv/cache.py:54-61 (PagedKVCache.write) for one layer's caches
+    [num_blocks, block_size, Hkv, D]: index_copy_ of k and v at the slots, in place."""
+    slots = slot_mapping.to(device=k_cache.device, dtype=torch.long)
+    flat = (-1, k.shape[1], k.shape[2])
+    k_cache.view(flat).index_copy_(0, slots, k.to(k_cache.dtype))
+    v_cache.view(flat).index_copy_(0, slots, v.to(v_cache.dtype))
+
+
+def latent_cache_write(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
+    """emberserve/kv/cache.py:152-157 (PagedLatentCache.write) for one layer's cache
+    [num_blocks, block_size, latent_dim]."""
+    slots = slot_mapping.to(device=cache.device, dtype=torch.long)
+    cache.view(-1, latent.shape[-1]).index_copy_(0, slots, latent.to(cache.dtype))

@@ -28,7 +28,8 @@ def _declared() -> list[str]:
 def test_header_declares_the_entry_points():
     names = _declared()
     for n in ["ember_rmsnorm", "ember_fused_add_rmsnorm", "ember_rope", "ember_silu_and_mul",
-              "ember_embedding", "ember_qk_norm_rope", "ember_mla_latent_rope"]:
+              "ember_embedding", "ember_qk_norm_rope", "ember_mla_latent_rope", "ember_kv_cache_write",
+              "ember_latent_cache_write"]:
         assert n in names
 
 
@@ -67,6 +68,12 @@ def test_argument_validation_happens_before_any_launch():
     assert lib.ember_rope(p, 64, 64, 1, p, 64, 64, 1, 64, p, p, 8, 64, p, 0, 2, None) == 0
     assert lib.ember_mla_latent_rope(p, 576, 512, p, 576, p, 192, 192, 16, 64, p, 2, 1e-6, p, p, 8, 64,
                                      p, 4, p, 500, 2, None) == 1  # latent row too short
+    assert lib.ember_kv_cache_write(p, 1024, 128, p, 1024, 128, 8, 128, p, 4, p, p, 64, 1024, 128, 3,
+                                    None) == 1  # elem_bytes 3
+    assert lib.ember_kv_cache_write(p, 1024, 128, p, 1024, 128, 8, 128, p, 0, p, p, 64, 1024, 128, 2,
+                                    None) == 0  # no tokens
+    assert lib.ember_latent_cache_write(p, 576, 0, p, 4, p, 64, 576, 2, None) == 1  # latent_dim 0
+    assert lib.ember_latent_cache_write(p, 576, 576, p, 0, p, 64, 576, 2, None) == 0
 
 
 def test_ops_api_mirrors_the_reference():
@@ -75,6 +82,24 @@ def test_ops_api_mirrors_the_reference():
                  "qk_norm_rope", "mla_latent_rope", "embedding"]:
         assert callable(getattr(ops, name)), name
     assert callable(rope.RotaryEmbedding) and callable(rope.rotate_half)
+
+
+def test_cache_writes_on_cpu_match_the_oracle():
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(5, 2, 32, generator=g)
+    v = torch.randn(5, 2, 32, generator=g)
+    slots = torch.tensor([3, 9, 0, 15, 4])
+    a = [torch.zeros(4, 4, 2, 32) for _ in range(2)]
+    b = [torch.zeros(4, 4, 2, 32) for _ in range(2)]
+    ops.kv_cache_write(k, v, slots, *a)
+    ref.kv_cache_write(k, v, slots, *b)
+    assert_bitexact(a[0], b[0])
+    assert_bitexact(a[1], b[1])
+    lat = torch.randn(5, 48, generator=g)
+    c1, c2 = torch.zeros(4, 4, 48), torch.zeros(4, 4, 48)
+    ops.latent_cache_write(lat, slots, c1)
+    ref.latent_cache_write(lat, slots, c2)
+    assert_bitexact(c1, c2)
 
 
 def test_dispatch_uses_torch_off_gpu():
@@ -166,6 +191,10 @@ def test_hip_wrappers_refuse_host_tensors():
         ops.qk_norm_rope_hip(q, q, w, w, 1e-6, cos, sin, pos)
     with pytest.raises(ValueError):
         ops.mla_latent_rope_hip(x, x[:, :16], q[..., :16], w, 1e-6, cos, sin, pos)
+    with pytest.raises(ValueError):
+        ops.kv_cache_write_hip(q, q, pos, torch.zeros(2, 4, 1, 64), torch.zeros(2, 4, 1, 64))
+    with pytest.raises(ValueError):
+        ops.latent_cache_write_hip(x, pos, torch.zeros(2, 4, 64))
 
 
 def test_silu_and_mul_rejects_odd_width():

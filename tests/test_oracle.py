@@ -283,3 +283,36 @@ def test_ulp_helper_counts_ulps():
     a = torch.tensor([1.0, -1.0, 0.0], dtype=torch.float16)
     b = torch.tensor([1.0 + 2 ** -10, -1.0 - 2 * 2 ** -10, -0.0], dtype=torch.float16)
     assert ulp_diff(a, b).tolist() == [1, 2, 0]
+
+
+# ---------------------------------------------------------------- KV-cache writes
+
+def test_kv_cache_write_matches_slot_loop():
+    g = torch.Generator().manual_seed(9)
+    n, hk, d, blocks, bs = 10, 2, 16, 4, 8
+    k = torch.randn(n, hk, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hk, d, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(blocks * bs, generator=g)[:n]
+    kc = torch.zeros(blocks, bs, hk, d, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    ref.kv_cache_write(k, v, slots, kc, vc)
+    want_k = torch.zeros_like(kc).view(-1, hk, d)
+    want_v = torch.zeros_like(vc).view(-1, hk, d)
+    for t in range(n):
+        want_k[int(slots[t])] = k[t]
+        want_v[int(slots[t])] = v[t]
+    assert_bitexact(kc.view(-1, hk, d), want_k)
+    assert_bitexact(vc.view(-1, hk, d), want_v)
+
+
+def test_latent_cache_write_matches_slot_loop():
+    g = torch.Generator().manual_seed(10)
+    n, dim = 7, 576
+    lat = torch.randn(n, dim, generator=g).to(torch.bfloat16)
+    slots = torch.tensor([5, 0, 31, 8, 9, 17, 2])
+    cache = torch.zeros(4, 8, dim, dtype=torch.bfloat16)
+    ref.latent_cache_write(lat, slots, cache)
+    want = torch.zeros(32, dim, dtype=torch.bfloat16)
+    for t in range(n):
+        want[int(slots[t])] = lat[t]
+    assert_bitexact(cache.view(-1, dim), want)

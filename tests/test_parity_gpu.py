@@ -607,3 +607,70 @@ def test_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         for g, wv, name in zip(got, want, ["normed", "residual", "act", "qkv"]):
             assert_bitexact(g, wv, f"replay {seed} {name}")
+
+
+# ---------------------------------------------------------------- paged KV-cache writes
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hk,d", [(8, 128), (4, 128), (2, 64), (1, 6)])
+def test_kv_cache_write_bitexact(dtype, hk, d):
+    """k, v as views of a fused qkv buffer scattered into [blocks, block_size, Hkv, D]
+    caches (kv/cache.py:54-61); unwritten slots keep their contents. (1, 6) takes the
+    scalar path (12-byte rows)."""
+    n, hq, blocks, bs = 100, 4, 16, 16
+    _say(f"kv_cache_write {dtype} hk={hk} d={d}")
+    g = torch.Generator().manual_seed(90)
+    qkv = _rand(n, (hq + 2 * hk) * d, dtype=dtype, seed=91)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    v = qkv[:, (hq + hk) * d:].view(n, hk, d)
+    slots = torch.randperm(blocks * bs, generator=g)[:n]
+    kc0 = _rand(blocks, bs, hk, d, dtype=dtype, seed=92)  # stale contents must survive where unwritten
+    vc0 = _rand(blocks, bs, hk, d, dtype=dtype, seed=93)
+    want_k, want_v = kc0.clone(), vc0.clone()
+    ref.kv_cache_write(k, v, slots, want_k, want_v)
+    qkv_d = qkv.to(DEV)
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    ops.kv_cache_write_hip(qkv_d[:, hq * d:(hq + hk) * d].view(n, hk, d), qkv_d[:, (hq + hk) * d:].view(n, hk, d),
+                           slots.to(DEV), kc, vc)
+    assert_bitexact(kc, want_k, "k cache")
+    assert_bitexact(vc, want_v, "v cache")
+
+
+def test_kv_cache_write_qwen3_prefill_and_bad_slot(monkeypatch):
+    """Qwen3-8B prefill shape (8 kv heads x 128, T = 8192) into a 1024-block cache, then a
+    slot past the end: skipped, and IndexError under EMBERSERVE_CHECK_INDICES=1."""
+    n, hk, d, blocks, bs = 8192, 8, 128, 1024, 16
+    g = torch.Generator().manual_seed(94)
+    k = _rand(n, hk, d, dtype=torch.bfloat16, seed=95)
+    v = _rand(n, hk, d, dtype=torch.bfloat16, seed=96)
+    slots = torch.randperm(blocks * bs, generator=g)[:n]
+    want_k = torch.zeros(blocks, bs, hk, d, dtype=torch.bfloat16)
+    want_v = torch.zeros_like(want_k)
+    ref.kv_cache_write(k, v, slots, want_k, want_v)
+    kc = torch.zeros(blocks, bs, hk, d, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    ops.kv_cache_write_hip(k.to(DEV), v.to(DEV), slots.to(DEV), kc, vc)
+    assert_bitexact(kc, want_k, "k cache")
+    assert_bitexact(vc, want_v, "v cache")
+    bad = slots[:4].clone()
+    bad[2] = blocks * bs
+    monkeypatch.setenv("EMBERSERVE_CHECK_INDICES", "1")
+    kc2 = torch.zeros_like(kc)
+    with pytest.raises(IndexError):
+        ops.kv_cache_write_hip(k[:4].to(DEV), v[:4].to(DEV), bad.to(DEV), kc2, torch.zeros_like(kc2))
+    assert int(torch.count_nonzero(kc2.view(-1, hk, d)[bad[[0, 1, 3]].to(DEV)].float() == 0)) < 3 * hk * d
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_latent_cache_write_bitexact(dtype):
+    """MLA latent rows [T, 576] (and a view with row stride 3648) into [blocks, bs, 576]."""
+    n, dim, blocks, bs = 500, 576, 64, 16
+    g = torch.Generator().manual_seed(97)
+    buf = _rand(n, 3648, dtype=dtype, seed=98)
+    slots = torch.randperm(blocks * bs, generator=g)[:n]
+    for lat, lat_d in [(buf[:, 3072:], buf.to(DEV)[:, 3072:]), (buf[:, :dim].contiguous(), buf[:, :dim].contiguous().to(DEV))]:
+        want = torch.zeros(blocks, bs, dim, dtype=dtype)
+        ref.latent_cache_write(lat, slots, want)
+        cache = torch.zeros(blocks, bs, dim, dtype=dtype, device=DEV)
+        ops.latent_cache_write_hip(lat_d, slots.to(DEV), cache)
+        assert_bitexact(cache, want, "latent cache")
