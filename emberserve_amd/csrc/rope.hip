@@ -144,6 +144,92 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
   if (bad && j == 0 && hg == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
 }
 
+// Rope (optionally with the Qwen3 qk-norm) fused with the paged KV-cache write that
+// consumes it (qwen2.py:95-101 then kv/cache.py:54-61): per token the Hq + 2 Hkv head rows
+// are q heads (rotated in place), k heads (rotated in place and stored to k_cache[slot])
+// and v heads (copied to v_cache[slot]). Same mapping and load discipline as k_rope with
+// one head per lane; the k rows are not read back for the cache write.
+template <typename T, typename WT, int VEC, int J, bool NORM, bool WAVE_TOK>
+__global__ void __launch_bounds__(kRopeBlock)
+k_rope_kv(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, int64_t kts, int64_t khs,
+          int hk, const T* __restrict__ v, int64_t vts, int64_t vhs, int half, const WT* __restrict__ qw,
+          const WT* __restrict__ kw, float eps, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+          int64_t trows, int64_t tstride, const int64_t* __restrict__ pos, const int64_t* __restrict__ slots,
+          T* __restrict__ kc, T* __restrict__ vc, int64_t num_slots, int64_t css, int64_t chs, uint32_t ntok,
+          FastDiv hdiv, uint32_t* __restrict__ err) {
+  const uint32_t gt = blockIdx.x * static_cast<uint32_t>(kRopeBlock) + threadIdx.x;
+  const uint32_t j = gt % J;
+  const uint32_t rowid = gt / J;
+  uint32_t tok = hdiv.div(rowid);  // head rows per token: hq + 2 hk
+  if constexpr (WAVE_TOK) tok = __builtin_amdgcn_readfirstlane(tok);
+  if (tok >= ntok) return;
+  const int h = static_cast<int>(rowid - tok * hdiv.d);
+  const int kind = h < hq ? 0 : (h < hq + hk ? 1 : 2);  // q, k, v: uniform across the J lanes
+  const int hh = kind == 0 ? h : (kind == 1 ? h - hq : h - hq - hk);
+  const int64_t off = static_cast<int64_t>(j) * VEC;
+
+  const int64_t p = pos[tok];
+  const int64_t slot = slots[tok];
+  T* ptr = kind == 0 ? q + tok * qts + hh * qhs : k + tok * kts + hh * khs;
+  const T* src = (kind == 2 ? v + tok * vts + hh * vhs : ptr) + off;
+  const Pack<T, VEC> x1 = load_stream<T, VEC>(src);
+  const Pack<T, VEC> x2 = load_stream<T, VEC>(src + half);
+  const bool bad = p < 0 || p >= trows;
+  const int64_t pc = bad ? 0 : p;
+  float c[VEC];
+  float s[VEC];
+  load_vals<float, VEC>(cos_t + pc * tstride + off, c);
+  load_vals<float, VEC>(sin_t + pc * tstride + off, s);
+  Pack<WT, VEC> wp1, wp2;
+  if constexpr (NORM) {
+    const WT* w0 = kind == 0 ? qw : kw;
+    wp1 = load_pack<WT, VEC>(w0 + off);
+    wp2 = load_pack<WT, VEC>(w0 + half + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before any arithmetic
+
+  Pack<T, VEC> o1 = x1;
+  Pack<T, VEC> o2 = x2;
+  if (kind != 2) {
+    float f1[VEC];
+    float f2[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      f1[e] = to_f32(x1.v[e]);
+      f2[e] = to_f32(x2.v[e]);
+    }
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss += f1[e] * f1[e] + f2[e] * f2[e];
+      const float tot = group_sum<J>(ss);
+      const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        f1[e] = round_to<T>(round_to<T>(f1[e] * inv) * to_f32(wp1.v[e]));
+        f2[e] = round_to<T>(round_to<T>(f2[e] * inv) * to_f32(wp2.v[e]));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      o1.v[e] = bad ? x1.v[e] : from_f32<T>(f1[e] * c[e] - f2[e] * s[e]);
+      o2.v[e] = bad ? x2.v[e] : from_f32<T>(f2[e] * c[e] + f1[e] * s[e]);
+    }
+    store_stream<T, VEC>(ptr + off, o1);
+    store_stream<T, VEC>(ptr + off + half, o2);
+  }
+  const bool slot_ok = slot >= 0 && slot < num_slots;
+  if (kind != 0 && slot_ok) {
+    T* dst = (kind == 1 ? kc : vc) + slot * css + hh * chs + off;
+    store_stream<T, VEC>(dst, o1);
+    store_stream<T, VEC>(dst + half, o2);
+  }
+  if (j == 0 && h == 0) {
+    if (bad) atomicOr(err, EMBER_ERR_ROPE_POS);
+    if (!slot_ok) atomicOr(err, EMBER_ERR_KV_SLOT);
+  }
+}
+
 // Any head_dim, any alignment: one wave per (token, head), scalar accesses, loops over the
 // half dimension (the norm variant reads the row twice, the second time from cache).
 template <typename T, typename WT, bool NORM>
@@ -283,6 +369,64 @@ int check_rope_args(const RopeArgs& a) {
   if (a.hq > 0 && a.q == nullptr) return EMBER_EINVAL;
   if (a.hk > 0 && a.k == nullptr) return EMBER_EINVAL;
   return EMBER_OK;
+}
+
+struct RopeKvArgs {
+  RopeArgs r;
+  const void* v;
+  int64_t vts, vhs;
+  const int64_t* slots;
+  void* kc;
+  void* vc;
+  int64_t num_slots, css, chs;
+};
+
+template <typename T, typename WT, int VEC, int J, bool NORM>
+int launch_rope_kv_vec(const RopeKvArgs& a) {
+  const RopeArgs& r = a.r;
+  const int64_t per_tok = r.hq + 2 * r.hk;
+  const int64_t threads = r.ntok * per_tok * J;
+  if (threads > 0x7fffffffLL) return EMBER_EINVAL;
+  const int64_t grid = cdiv(threads, kRopeBlock);
+  const FastDiv hdiv = FastDiv::make(static_cast<uint32_t>(per_tok));
+#define EMBER_LAUNCH_ROPE_KV(WT_)                                                                             \
+  hipLaunchKernelGGL((k_rope_kv<T, WT, VEC, J, NORM, WT_>), dim3(static_cast<uint32_t>(grid)), dim3(kRopeBlock), 0, \
+                     r.stream, static_cast<T*>(r.q), r.qts, r.qhs, static_cast<int>(r.hq), static_cast<T*>(r.k),     \
+                     r.kts, r.khs, static_cast<int>(r.hk), static_cast<const T*>(a.v), a.vts, a.vhs,                \
+                     static_cast<int>(r.head_dim / 2), static_cast<const WT*>(r.qw), static_cast<const WT*>(r.kw),    \
+                     r.eps, r.cos_t, r.sin_t, r.trows, r.tstride, r.pos, a.slots, static_cast<T*>(a.kc),           \
+                     static_cast<T*>(a.vc), a.num_slots, a.css, a.chs, static_cast<uint32_t>(r.ntok), hdiv, r.err)
+  if ((per_tok * J) % kWave == 0) {
+    EMBER_LAUNCH_ROPE_KV(true);
+  } else {
+    EMBER_LAUNCH_ROPE_KV(false);
+  }
+#undef EMBER_LAUNCH_ROPE_KV
+  return launch_status();
+}
+
+template <typename T, typename WT, bool NORM>
+int launch_rope_kv_typed(const RopeKvArgs& a) {
+  constexpr int VEC = 16 / sizeof(T);
+  const RopeArgs& r = a.r;
+  const int64_t half = r.head_dim / 2;
+  const int64_t j = half / VEC;
+  const bool vec_ok = half % VEC == 0 && (j & (j - 1)) == 0 && j >= 1 && j <= 32 && aligned16(r.q) &&
+                      aligned16(r.k) && aligned16(a.v) && aligned16(a.kc) && aligned16(a.vc) &&
+                      aligned16(r.cos_t) && aligned16(r.sin_t) && r.tstride % 4 == 0 && r.qts % VEC == 0 &&
+                      r.qhs % VEC == 0 && r.kts % VEC == 0 && r.khs % VEC == 0 && a.vts % VEC == 0 &&
+                      a.vhs % VEC == 0 && a.css % VEC == 0 && a.chs % VEC == 0 &&
+                      (!NORM || (aligned16(r.qw) && aligned16(r.kw)));
+  if (!vec_ok) return EMBER_EALIGN;  // the caller runs the two unfused ops instead
+  switch (j) {
+    case 1: return launch_rope_kv_vec<T, WT, VEC, 1, NORM>(a);
+    case 2: return launch_rope_kv_vec<T, WT, VEC, 2, NORM>(a);
+    case 4: return launch_rope_kv_vec<T, WT, VEC, 4, NORM>(a);
+    case 8: return launch_rope_kv_vec<T, WT, VEC, 8, NORM>(a);
+    case 16: return launch_rope_kv_vec<T, WT, VEC, 16, NORM>(a);
+    case 32: return launch_rope_kv_vec<T, WT, VEC, 32, NORM>(a);
+    default: return EMBER_EALIGN;
+  }
 }
 
 // ---------------------------------------------------------------- MLA latent path
@@ -645,6 +789,45 @@ int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora
     case EMBER_F32: return launch_mla_typed<float, float>(a);
     case EMBER_F16: return wf ? launch_mla_typed<_Float16, float>(a) : launch_mla_typed<_Float16, _Float16>(a);
     case EMBER_BF16: return wf ? launch_mla_typed<__bf16, float>(a) : launch_mla_typed<__bf16, __bf16>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
+int ember_rope_kv_cache(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads, void* k,
+                        int64_t k_token_stride, int64_t k_head_stride, int64_t num_kv_heads, const void* v,
+                        int64_t v_token_stride, int64_t v_head_stride, int64_t head_dim, const void* q_weight,
+                        const void* k_weight, int weight_dtype, float eps, const float* cos_table,
+                        const float* sin_table, int64_t table_rows, int64_t table_row_stride,
+                        const int64_t* positions, const int64_t* slot_mapping, int64_t num_tokens, void* k_cache,
+                        void* v_cache, int64_t num_slots, int64_t cache_slot_stride, int64_t cache_head_stride,
+                        int dtype, void* stream) {
+  using namespace ember;
+  RopeKvArgs a{RopeArgs{q,        q_token_stride, q_head_stride, num_q_heads, k,        k_token_stride,
+                        k_head_stride, num_kv_heads, head_dim, q_weight,    k_weight, eps,
+                        cos_table, sin_table, table_rows, table_row_stride, positions, num_tokens,
+                        static_cast<hipStream_t>(stream), nullptr},
+               v, v_token_stride, v_head_stride, slot_mapping, k_cache, v_cache, num_slots, cache_slot_stride,
+               cache_head_stride};
+  const int st = check_rope_args(a.r);
+  if (st < 0) return EMBER_OK;
+  if (st != EMBER_OK) return st;
+  if (num_kv_heads <= 0 || v == nullptr || k == nullptr || slot_mapping == nullptr || k_cache == nullptr ||
+      v_cache == nullptr || num_slots < 0 || num_tokens > 0x7fffffffLL)
+    return EMBER_EINVAL;
+  const bool norm = q_weight != nullptr;
+  if (norm && (k_weight == nullptr || (weight_dtype != dtype && weight_dtype != EMBER_F32))) return EMBER_EINVAL;
+  a.r.err = device_error_word();
+  if (a.r.err == nullptr) return EMBER_ENODEV;
+  const bool wf = norm && weight_dtype == EMBER_F32 && dtype != EMBER_F32;
+  switch (dtype) {
+    case EMBER_F32:
+      return norm ? launch_rope_kv_typed<float, float, true>(a) : launch_rope_kv_typed<float, float, false>(a);
+    case EMBER_F16:
+      if (!norm) return launch_rope_kv_typed<_Float16, _Float16, false>(a);
+      return wf ? launch_rope_kv_typed<_Float16, float, true>(a) : launch_rope_kv_typed<_Float16, _Float16, true>(a);
+    case EMBER_BF16:
+      if (!norm) return launch_rope_kv_typed<__bf16, __bf16, false>(a);
+      return wf ? launch_rope_kv_typed<__bf16, float, true>(a) : launch_rope_kv_typed<__bf16, __bf16, true>(a);
     default: return EMBER_EINVAL;
   }
 }

@@ -51,7 +51,7 @@ __all__ = [
     "rmsnorm_torch", "fused_add_rmsnorm_torch", "rope_torch", "silu_and_mul_torch",
     "embedding_torch", "qk_norm_rope_torch", "mla_latent_rope_torch",
     "kv_cache_write", "latent_cache_write", "kv_cache_write_hip", "latent_cache_write_hip",
-    "kv_cache_write_torch", "latent_cache_write_torch",
+    "kv_cache_write_torch", "latent_cache_write_torch", "rope_kv_cache", "rope_kv_cache_hip",
 ]
 
 
@@ -355,6 +355,70 @@ def latent_cache_write_hip(latent: torch.Tensor, slot_mapping: torch.Tensor, cac
         _raise_index_errors()
 
 
+def rope_kv_cache_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                      sin: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                      k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      q_weight: torch.Tensor | None = None, k_weight: torch.Tensor | None = None,
+                      eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    """rope (after the Qwen3 q/k RMSNorm when q_weight/k_weight are given), in place on the
+    q/k views, fused with the paged KV-cache write of the rotated k and of v: one kernel
+    for qwen2.py:95-101 followed by PagedKVCache.write (kv/cache.py:54-61). Returns (q, k).
+    Operands the fused kernel cannot take (misaligned views, odd head sizes) run the two
+    unfused HIP ops, with the same result."""
+    tensors = [q, k, v, cos, sin, positions, slot_mapping, k_cache, v_cache]
+    norm = q_weight is not None
+    if norm:
+        if k_weight is None:
+            raise ValueError("rope_kv_cache: k_weight is required with q_weight")
+        tensors += [q_weight, k_weight]
+    _require_device("rope_kv_cache", *tensors)
+    n, h, d = q.shape
+    hk = k.shape[1]
+    if not (q.stride(2) == 1 and k.stride(2) == 1 and v.stride(2) == 1 and d % 2 == 0):
+        raise AssertionError("rope_kv_cache: unit stride in the head dim and an even head_dim required")
+    if k.shape != (n, hk, d) or v.shape != k.shape or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("rope_kv_cache: q [N, H, D], k and v [N, Hkv, D] of one dtype expected")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.stride() != v_cache.stride() or tuple(k_cache.shape[-2:]) != (hk, d):
+        raise ValueError("rope_kv_cache: k_cache and v_cache must be [..., Hkv, D] caches of q's dtype")
+    if slot_mapping.numel() != n:
+        raise ValueError("rope_kv_cache: one slot per token expected")
+    if n == 0:
+        return q, k
+    cos, sin, positions = _tables(cos, sin, positions, d)
+    slots = (slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.long()).contiguous()
+    kc = k_cache.view(-1, hk, d)
+    wtag, qw_ptr, kw_ptr = 0, None, None
+    if norm:
+        if q_weight.numel() != d or k_weight.numel() != d:
+            raise ValueError("rope_kv_cache: q/k norm weights must have head_dim elements")
+        qw, wtag = _weight_for(q_weight, q)
+        kw, ktag = _weight_for(k_weight, q)
+        if ktag != wtag:
+            qw, kw, wtag = qw.float(), kw.float(), _lib.F32
+        qw_ptr, kw_ptr = qw.data_ptr(), kw.data_ptr()
+    lib = _lib.load()
+    idx = q.device.index
+    with torch.cuda.device(idx):
+        st = lib.ember_rope_kv_cache(
+            q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0), k.stride(1), hk, v.data_ptr(),
+            v.stride(0), v.stride(1), d, qw_ptr, kw_ptr, wtag, float(eps), cos.data_ptr(), sin.data_ptr(),
+            cos.shape[0], cos.stride(0), positions.data_ptr(), slots.data_ptr(), n, k_cache.data_ptr(),
+            v_cache.data_ptr(), kc.shape[0], kc.stride(0), kc.stride(1), _lib.dtype_tag(q.dtype),
+            torch._C._cuda_getCurrentRawStream(idx))
+    if st == 2:  # EMBER_EALIGN: the unfused pair
+        if norm:
+            qk_norm_rope_hip(q, k, q_weight, k_weight, eps, cos, sin, positions)
+        else:
+            rope_hip(q, k, cos, sin, positions)
+        kv_cache_write_hip(k, v, slots, k_cache, v_cache)
+        return q, k
+    _lib.check(st, "ember_rope_kv_cache")
+    if _check_indices():
+        _raise_index_errors()
+    return q, k
+
+
 # ---- dispatch (ops.py:92-115 plus the fused additions) ----------------------------------
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -416,3 +480,18 @@ def latent_cache_write(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: 
     if fused_enabled(latent):
         return latent_cache_write_hip(latent, slot_mapping, cache)
     return latent_cache_write_torch(latent, slot_mapping, cache)
+
+
+def rope_kv_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  positions: torch.Tensor, slot_mapping: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, q_weight: torch.Tensor | None = None,
+                  k_weight: torch.Tensor | None = None, eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    if fused_enabled(q):
+        return rope_kv_cache_hip(q, k, v, cos, sin, positions, slot_mapping, k_cache, v_cache, q_weight,
+                                 k_weight, eps)
+    if q_weight is not None:
+        q, k = qk_norm_rope_torch(q, k, q_weight, k_weight, eps, cos, sin, positions)
+    else:
+        q, k = rope_torch(q, k, cos, sin, positions)
+    kv_cache_write_torch(k, v, slot_mapping, k_cache, v_cache)
+    return q, k

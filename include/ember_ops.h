@@ -36,6 +36,9 @@
  *                             emberserve/model/deepseek.py:124-133
  *   ember_kv_cache_write      PagedKVCache.write, emberserve/kv/cache.py:54-61
  *   ember_latent_cache_write  PagedLatentCache.write, emberserve/kv/cache.py:152-157
+ *   ember_rope_kv_cache       rotary_emb (with the Qwen3 q/k norm when weights are given)
+ *                             followed by PagedKVCache.write: qwen2.py:95-101 and the
+ *                             backends' cache.write (attn/paged_triton.py:477)
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
@@ -54,7 +57,7 @@ extern "C" {
 /* status codes */
 #define EMBER_OK 0
 #define EMBER_EINVAL 1      /* bad shape, stride, dtype or pointer */
-#define EMBER_EALIGN 2      /* reserved: misalignment is handled by scalar kernels */
+#define EMBER_EALIGN 2      /* a fused entry point's operands are not 16-byte aligned: run the unfused ops */
 #define EMBER_ELAUNCH 3     /* the HIP launch itself failed */
 #define EMBER_ENODEV 4      /* no HIP device / runtime call failed */
 
@@ -178,6 +181,25 @@ int ember_latent_cache_write(const void* latent, int64_t latent_token_stride, in
                              const int64_t* slot_mapping, int64_t num_tokens,
                              void* cache, int64_t num_slots, int64_t cache_slot_stride,
                              int64_t elem_bytes, void* stream);
+
+/* Rope (and, when q_weight != NULL, the Qwen3 per-head q/k RMSNorm before it) fused with
+ * the paged KV-cache write that follows it: q and k are transformed in place exactly as by
+ * ember_qk_norm_rope / ember_rope, then the transformed k rows and the v rows are stored
+ * at slot_mapping[t] of k_cache / v_cache as ember_kv_cache_write stores them. v is
+ * [tokens, num_kv_heads, head_dim] (read only). Needs 16-byte aligned operands and strides
+ * and head_dim / 2 a power-of-two multiple of 16 bytes; otherwise returns EMBER_EALIGN and
+ * does nothing, and the caller runs the two unfused entry points. */
+int ember_rope_kv_cache(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads,
+                        void* k, int64_t k_token_stride, int64_t k_head_stride, int64_t num_kv_heads,
+                        const void* v, int64_t v_token_stride, int64_t v_head_stride,
+                        int64_t head_dim,
+                        const void* q_weight, const void* k_weight, int weight_dtype, float eps,
+                        const float* cos_table, const float* sin_table,
+                        int64_t table_rows, int64_t table_row_stride,
+                        const int64_t* positions, const int64_t* slot_mapping, int64_t num_tokens,
+                        void* k_cache, void* v_cache, int64_t num_slots,
+                        int64_t cache_slot_stride, int64_t cache_head_stride,
+                        int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -674,3 +674,77 @@ def test_latent_cache_write_bitexact(dtype):
         cache = torch.zeros(blocks, bs, dim, dtype=dtype, device=DEV)
         ops.latent_cache_write_hip(lat_d, slots.to(DEV), cache)
         assert_bitexact(cache, want, "latent cache")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("heads,d", [((32, 8), 128), ((28, 4), 128), ((14, 2), 64)])
+def test_rope_kv_cache_fused(dtype, norm, heads, d):
+    """rope (+ Qwen3 qk-norm) then PagedKVCache.write, in one kernel: q/k in place as the
+    unfused ops leave them, the cache holds exactly the in-place k rows and the v rows."""
+    hq, hk = heads
+    n, blocks, bs = 64, 16, 16
+    _say(f"rope_kv_cache {dtype} norm={norm} heads={heads} d={d}")
+    qkv, qw, kw, pos = gen.qkv_inputs(n, hq, hk, d, 4096, dtype, seed=100)
+    cos, sin = _tables(d, 4096, 1e6)
+    slots = torch.randperm(blocks * bs, generator=torch.Generator().manual_seed(101))[:n]
+    q = qkv[:, :hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    v = qkv[:, (hq + hk) * d:].view(n, hk, d)
+    if norm:
+        want_q, want_k = ref.qk_norm_rope(q, k, qw, kw, 1e-6, cos, sin, pos)
+    else:
+        want_q, want_k = ref.rope(q, k, cos, sin, pos)
+    want_kc = torch.zeros(blocks, bs, hk, d, dtype=dtype)
+    want_vc = torch.zeros_like(want_kc)
+    ref.kv_cache_write(want_k, v, slots, want_kc, want_vc)
+
+    qkv_d = qkv.to(DEV)
+    qd = qkv_d[:, :hq * d].view(n, hq, d)
+    kd = qkv_d[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    vd = qkv_d[:, (hq + hk) * d:].view(n, hk, d)
+    kc = torch.zeros(blocks, bs, hk, d, dtype=dtype, device=DEV)
+    vc = torch.zeros_like(kc)
+    ops.rope_kv_cache_hip(qd, kd, vd, cos.to(DEV), sin.to(DEV), pos.to(DEV), slots.to(DEV), kc, vc,
+                          qw.to(DEV) if norm else None, kw.to(DEV) if norm else None, 1e-6)
+    if norm:
+        _check_qk(qd, kd, want_q, want_k, q, k, qw, kw, cos, sin, pos, ULP[dtype])
+    else:
+        assert_bitexact(qd, want_q, "q")
+        assert_bitexact(kd, want_k, "k")
+    # the cache holds exactly the in-place k rows (same bits), and exactly v
+    assert_bitexact(kc.view(-1, hk, d)[slots.to(DEV)], kd, "k cache rows == rotated k")
+    assert_bitexact(vc, want_vc, "v cache")
+    assert_bitexact(vd, v, "v untouched")
+    untouched = torch.ones(blocks * bs, dtype=torch.bool)
+    untouched[slots] = False
+    assert not bool(kc.view(-1, hk, d)[untouched.to(DEV)].any()), "unwritten slots stay zero"
+
+
+def test_rope_kv_cache_unaligned_falls_back():
+    """Views offset by one element: the fused kernel refuses (EMBER_EALIGN) and the wrapper
+    runs rope + kv write; same result as the oracle composition."""
+    n, hq, hk, d = 12, 4, 2, 64
+    dt = torch.bfloat16
+    qkv = _rand(n, 1 + (hq + 2 * hk) * d, dtype=dt, seed=102)
+    cos, sin = _tables(d, 256, 1e4)
+    pos = torch.randint(0, 256, (n,), generator=torch.Generator().manual_seed(103))
+    slots = torch.randperm(64, generator=torch.Generator().manual_seed(104))[:n]
+
+    def views(buf):
+        return (buf[:, 1:1 + hq * d].view(n, hq, d), buf[:, 1 + hq * d:1 + (hq + hk) * d].view(n, hk, d),
+                buf[:, 1 + (hq + hk) * d:].view(n, hk, d))
+
+    q, k, v = views(qkv)
+    want_q, want_k = ref.rope(q, k, cos, sin, pos)
+    want_kc = torch.zeros(4, 16, hk, d, dtype=dt)
+    want_vc = torch.zeros_like(want_kc)
+    ref.kv_cache_write(want_k, v, slots, want_kc, want_vc)
+    buf = qkv.to(DEV)
+    qd, kd, vd = views(buf)
+    kc = torch.zeros(4, 16, hk, d, dtype=dt, device=DEV)
+    vc = torch.zeros_like(kc)
+    ops.rope_kv_cache_hip(qd, kd, vd, cos.to(DEV), sin.to(DEV), pos.to(DEV), slots.to(DEV), kc, vc)
+    assert_bitexact(qd, want_q, "q")
+    assert_bitexact(kc, want_kc, "k cache")
+    assert_bitexact(vc, want_vc, "v cache")
