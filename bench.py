@@ -102,7 +102,16 @@ def _cpu_factories():
         qv = q.view(t, 16, 192)
         return lambda: ref.mla_latent_rope(kv_a[:, :512], kv_a[:, 512:], qv[..., 128:], w, 1e-6, cos, sin, pos)
 
-    return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla)
+    def kv(t):
+        def build():
+            qkv, _, _, _ = gen.qkv_inputs(t, 32, 8, 128, 40960, torch.bfloat16)
+            slots = torch.randperm(2 * t, generator=gen.gen(5))[:t]
+            kc = torch.zeros(2 * t // 16, 16, 8, 128, dtype=torch.bfloat16)
+            return qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128), slots, kc, kc.clone()
+        k, v, slots, kc, vc = _cpu_inputs(("kv", t), build)
+        return lambda: ref.kv_cache_write(k, v, slots, kc, vc)
+
+    return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla, kv=kv)
 
 
 def _cpu_time_row(fn, budget_s):
@@ -200,6 +209,49 @@ def _ops(torch, ops, tables):
                       lambda a: ops.mla_latent_rope_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4]),
                       t * (576 + 3072 + 576) * 2, cpu=("mla", (t,)) if not in_model else None))
 
+    def kv_write(cfg, t):
+        blocks, bs = 2 * t // 16, 16  # a cache twice the batch, slots a random permutation
+
+        def make(i):
+            qkv = randn((t, 6144), bf, 50 + i)
+            g.manual_seed(60 + i)
+            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            kc = torch.zeros((blocks, bs, 8, 128), dtype=bf, device=dev)
+            return (qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128), slots, kc, torch.zeros_like(kc))
+        nbytes = 4 * t * 8 * 128 * 2 + 8 * t
+        out.append(Op("kv_cache_write", cfg, f"k,v[{t},8,128] bf16 -> paged cache", nbytes, make,
+                      lambda a: ops.kv_cache_write_hip(a[0], a[1], a[2], a[3], a[4]), 4 * t * 1024 * 2,
+                      cpu=("kv", (t,))))
+
+    def rope_kv(cfg, t):
+        cos, sin = tables(128, 40960, 1e6)
+        blocks, bs = 2 * t // 16, 16
+
+        def make(i):
+            qkv = randn((t, 6144), bf, 70 + i)
+            g.manual_seed(80 + i)
+            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            kc = torch.zeros((blocks, bs, 8, 128), dtype=bf, device=dev)
+            return (qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128),
+                    randint(t, 40960, 90 + i), slots, kc, torch.zeros_like(kc),
+                    randn((128,), bf, 91, 1.0, 0.1), randn((128,), bf, 92, 1.0, 0.1))
+        # q, k read + written in place, v read, k and v written to the cache, positions, slots
+        nbytes = 2 * t * 40 * 128 * 2 + t * 8 * 128 * 2 + 2 * t * 8 * 128 * 2 + 16 * t + 512
+        out.append(Op("qk_norm_rope_kv_cache", cfg, f"qkv[{t},6144] 32q+8kv x128 bf16 -> paged cache", nbytes, make,
+                      lambda a: ops.rope_kv_cache_hip(a[0], a[1], a[2], cos, sin, a[3], a[4], a[5], a[6], a[7], a[8],
+                                                      1e-6), t * 6144 * 2 + 4 * t * 1024 * 2))
+
+    def latent_write(cfg, t):
+        blocks, bs = 2 * t // 16, 16
+
+        def make(i):
+            g.manual_seed(95 + i)
+            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            return (randn((t, 576), bf, 96 + i), slots, torch.zeros((blocks, bs, 576), dtype=bf, device=dev))
+        nbytes = 2 * t * 576 * 2 + 8 * t
+        out.append(Op("latent_cache_write", cfg, f"latent[{t},576] bf16 -> paged cache", nbytes, make,
+                      lambda a: ops.latent_cache_write_hip(a[0], a[1], a[2]), 2 * t * 576 * 2))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -214,6 +266,11 @@ def _ops(torch, ops, tables):
         add_norm("4c", t, 4096, bf)
     mla("5", 8192, False)
     mla("5", 8192, True)
+    # The paged-cache consumers of the path (kv/cache.py:54-61, 152-157), Qwen3-8B / Moonlight
+    for t in (256, 8192):
+        kv_write("kv", t)
+        rope_kv("kv", t)
+    latent_write("kv", 8192)
     silu("extra", 8192, inter=12288, dtype=bf, label="silu_and_mul")  # Qwen3-8B MLP
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
@@ -498,6 +555,13 @@ def main() -> int:
                  row("silu_and_mul", "extra", 8192)]
         if all(p is not None for p in parts):
             us_per_layer["qwen3_8b_full_elementwise_set_T8192"] = round(sum(parts), 2)
+        # Qwen3-8B attention prologue: qk-norm + rope and the paged KV write, unfused vs fused
+        for tt in (256, 8192):
+            unf = [row("qk_norm_rope", "4b", tt), row("kv_cache_write", "kv", tt)]
+            fus = row("qk_norm_rope_kv_cache", "kv", tt)
+            if all(p is not None for p in unf) and fus is not None:
+                us_per_layer[f"qwen3_8b_qknorm_rope_kvwrite_T{tt}_unfused"] = round(sum(unf), 2)
+                us_per_layer[f"qwen3_8b_qknorm_rope_kvwrite_T{tt}_fused"] = round(fus, 2)
         # Qwen2.5-7B decoder layer's elementwise ops: 2 x add+RMSNorm (hidden 3584), rope
         # (28 q + 4 kv heads), silu_and_mul (I = 18944), as qwen2.py:140-159 runs them.
         for tt, rope_cfg in ((256, "2"), (8192, "7b")):
