@@ -252,6 +252,23 @@ def _ops(torch, ops, tables):
         out.append(Op("latent_cache_write", cfg, f"latent[{t},576] bf16 -> paged cache", nbytes, make,
                       lambda a: ops.latent_cache_write_hip(a[0], a[1], a[2]), 2 * t * 576 * 2))
 
+    def mla_cache(cfg, t):
+        cos, sin = tables(64, 8192, 5e4)
+        blocks, bs = 2 * t // 16, 16
+
+        def make(i):
+            kv_a = randn((t, 576), bf, 120 + i)
+            q = randn((t, 16, 192), bf, 130 + i)
+            g.manual_seed(140 + i)
+            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            return (kv_a[:, :512], kv_a[:, 512:], q[..., 128:], randn((512,), bf, 150, 1.0, 0.1),
+                    randint(t, 8192, 160 + i), slots, torch.zeros((blocks, bs, 576), dtype=bf, device=dev))
+        nbytes = t * 6408 + 1024 + t * (576 * 2 + 8)  # the MLA bytes + the cache rows and slots
+        out.append(Op("mla_latent_rope_cache", cfg, f"kv_a[{t},576] q[{t},16,192] bf16 -> paged cache + latent",
+                      nbytes, make,
+                      lambda a: ops.mla_latent_rope_cache_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4], a[5],
+                                                              a[6]), t * (576 * 3 + 3072) * 2))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -271,6 +288,7 @@ def _ops(torch, ops, tables):
         kv_write("kv", t)
         rope_kv("kv", t)
     latent_write("kv", 8192)
+    mla_cache("kv", 8192)
     silu("extra", 8192, inter=12288, dtype=bf, label="silu_and_mul")  # Qwen3-8B MLP
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
@@ -562,6 +580,11 @@ def main() -> int:
             if all(p is not None for p in unf) and fus is not None:
                 us_per_layer[f"qwen3_8b_qknorm_rope_kvwrite_T{tt}_unfused"] = round(sum(unf), 2)
                 us_per_layer[f"qwen3_8b_qknorm_rope_kvwrite_T{tt}_fused"] = round(fus, 2)
+        unf = [row("mla_latent_rope", "5", 8192), row("latent_cache_write", "kv", 8192)]
+        fus = row("mla_latent_rope_cache", "kv", 8192)
+        if all(p is not None for p in unf) and fus is not None:
+            us_per_layer["mla_latent_rope_cachewrite_T8192_unfused"] = round(sum(unf), 2)
+            us_per_layer["mla_latent_rope_cachewrite_T8192_fused"] = round(fus, 2)
         # Qwen2.5-7B decoder layer's elementwise ops: 2 x add+RMSNorm (hidden 3584), rope
         # (28 q + 4 kv heads), silu_and_mul (I = 18944), as qwen2.py:140-159 runs them.
         for tt, rope_cfg in ((256, "2"), (8192, "7b")):

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -46,6 +46,8 @@ SIGNATURES: dict[str, list] = {
     "ember_latent_cache_write": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
     "ember_rope_kv_cache": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _f32,
                             _p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "ember_mla_latent_rope_cache": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _f32,
+                                    _p, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i32, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],

@@ -439,13 +439,16 @@ int launch_rope_kv_typed(const RopeKvArgs& a) {
 // waves (J lanes per query head). A wave issues the loads of all its TPW tokens before any
 // arithmetic (the launcher uses TPW = 1; see launch_mla_vec).
 
-template <typename T, typename WT, int VEC, int J, int NVC, int TPW>
+template <typename T, typename WT, int VEC, int J, int NVC, int TPW, bool CACHE>
 __global__ void __launch_bounds__(kRopeBlock)
 k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
       int64_t qts, int64_t qhs, int H, int half, const WT* __restrict__ w, float eps,
       const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t trows, int64_t tstride,
       const int64_t* __restrict__ pos, int64_t ntok, T* __restrict__ lat, int64_t lts, int tasks_per_group,
+      const int64_t* __restrict__ slots, T* __restrict__ cache, int64_t num_slots, int64_t css,
       uint32_t* __restrict__ err) {
+  // CACHE: the latent rows also go to cache[slots[t]] (PagedLatentCache.write fused in);
+  // lat may then be null, and only the cache is written.
   // The task index is the same on every lane of a wave; readfirstlane makes that visible
   // to the compiler, so token indices live in SGPRs and the position is fetched with a
   // scalar load (its own counter, off the vector-load queue).
@@ -512,7 +515,16 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
       }
       const float tot = group_sum<kWave>(ss);
       const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
-      T* lrow = lat + toks[u] * lts;
+      T* lrow = lat == nullptr ? nullptr : lat + toks[u] * lts;
+      T* crow = nullptr;
+      if constexpr (CACHE) {
+        const int64_t slot = slots[toks[u]];
+        if (slot >= 0 && slot < num_slots) {
+          crow = cache + slot * css;
+        } else if (live && lane == 0) {
+          atomicOr(err, EMBER_ERR_KV_SLOT);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NVC; ++i) {
         const int vi = lane + i * kWave;
@@ -520,7 +532,8 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
           Pack<T, VEC> o;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(v[i][e] * inv) * to_f32(wv[i].v[e]));
-          store_stream<T, VEC>(lrow + static_cast<int64_t>(vi) * VEC, o);
+          if (lrow != nullptr) store_stream<T, VEC>(lrow + static_cast<int64_t>(vi) * VEC, o);
+          if (CACHE && crow != nullptr) store_stream<T, VEC>(crow + static_cast<int64_t>(vi) * VEC, o);
         }
       }
       if (live && lane < J) {
@@ -533,8 +546,14 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
           o1.v[e] = from_f32<T>(bad[u] ? 0.f : f1 * cc[u][e] - f2 * sn[u][e]);
           o2.v[e] = from_f32<T>(bad[u] ? 0.f : f2 * cc[u][e] + f1 * sn[u][e]);
         }
-        store_stream<T, VEC>(lrow + R + off, o1);
-        store_stream<T, VEC>(lrow + R + half + off, o2);
+        if (lrow != nullptr) {
+          store_stream<T, VEC>(lrow + R + off, o1);
+          store_stream<T, VEC>(lrow + R + half + off, o2);
+        }
+        if (CACHE && crow != nullptr) {
+          store_stream<T, VEC>(crow + R + off, o1);
+          store_stream<T, VEC>(crow + R + half + off, o2);
+        }
       }
       if (live && bad[u] && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
     }
@@ -643,6 +662,10 @@ struct MlaArgs {
   int64_t lts;
   hipStream_t stream;
   uint32_t* err;
+  const int64_t* slots = nullptr;  // the fused latent-cache write (null: none)
+  void* cache = nullptr;
+  int64_t num_slots = 0;
+  int64_t css = 0;
 };
 
 template <typename T, typename WT, int VEC, int J, int NVC>
@@ -653,11 +676,19 @@ int launch_mla_vec(const MlaArgs& a) {
   const int64_t tasks_per_group = 1 + cdiv(a.H * J, kWave);
   const int64_t grid = cdiv(cdiv(a.ntok, TPW) * tasks_per_group, kRopeBlock / kWave);
   if (grid * (kRopeBlock / kWave) > 0x7fffffffLL) return EMBER_EINVAL;  // task index is an int
-  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC, TPW>), dim3(static_cast<uint32_t>(grid)), dim3(kRopeBlock), 0, a.stream,
-                     static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
-                     static_cast<T*>(a.qpe), a.qts, a.qhs, static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2),
-                     static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok,
-                     static_cast<T*>(a.lat), a.lts, static_cast<int>(tasks_per_group), a.err);
+#define EMBER_LAUNCH_MLA(CACHE_)                                                                              \
+  hipLaunchKernelGGL((k_mla<T, WT, VEC, J, NVC, TPW, CACHE_>), dim3(static_cast<uint32_t>(grid)), dim3(kRopeBlock), 0, \
+                     a.stream, static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R),                          \
+                     static_cast<const T*>(a.kpe), a.kts, static_cast<T*>(a.qpe), a.qts, a.qhs,                  \
+                     static_cast<int>(a.H), static_cast<int>(a.rope_dim / 2), static_cast<const WT*>(a.w), a.eps,  \
+                     a.cos_t, a.sin_t, a.trows, a.tstride, a.pos, a.ntok, static_cast<T*>(a.lat), a.lts,           \
+                     static_cast<int>(tasks_per_group), a.slots, static_cast<T*>(a.cache), a.num_slots, a.css, a.err)
+  if (a.cache != nullptr) {
+    EMBER_LAUNCH_MLA(true);
+  } else {
+    EMBER_LAUNCH_MLA(false);
+  }
+#undef EMBER_LAUNCH_MLA
   return launch_status();
 }
 
@@ -682,7 +713,7 @@ int launch_mla_typed(const MlaArgs& a) {
                       j <= 16 && aligned16(a.c) && aligned16(a.kpe) && aligned16(a.qpe) && aligned16(a.lat) &&
                       aligned16(a.w) && aligned16(a.cos_t) && aligned16(a.sin_t) && a.tstride % 4 == 0 &&
                       a.cts % VEC == 0 && a.kts % VEC == 0 && a.qts % VEC == 0 && a.qhs % VEC == 0 &&
-                      a.lts % VEC == 0;
+                      a.lts % VEC == 0 && (a.cache == nullptr || (aligned16(a.cache) && a.css % VEC == 0));
   if (vec_ok) {
     const int nvc = pow2_ceil(cdiv(ncv, kWave));
     switch (j) {
@@ -694,6 +725,7 @@ int launch_mla_typed(const MlaArgs& a) {
       default: break;
     }
   }
+  if (a.cache != nullptr) return EMBER_EALIGN;  // the caller runs the unfused pair
   const int64_t grid = cdiv(a.ntok, 4);
   hipLaunchKernelGGL((k_mla_any<T, WT>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0, a.stream,
                      static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R), static_cast<const T*>(a.kpe), a.kts,
@@ -761,27 +793,40 @@ int ember_qk_norm_rope(void* q, int64_t q_token_stride, int64_t q_head_stride, i
   }
 }
 
-int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora_rank, const void* k_pe,
-                          int64_t k_pe_token_stride, void* q_pe, int64_t q_token_stride, int64_t q_head_stride,
-                          int64_t num_heads, int64_t rope_dim, const void* weight, int weight_dtype, float eps,
-                          const float* cos_table, const float* sin_table, int64_t table_rows,
-                          int64_t table_row_stride, const int64_t* positions, int64_t num_tokens, void* latent,
-                          int64_t latent_token_stride, int dtype, void* stream) {
-  using namespace ember;
+}  // extern "C"
+
+namespace ember {
+namespace {
+
+int mla_entry(const void* c, int64_t c_token_stride, int64_t kv_lora_rank, const void* k_pe,
+              int64_t k_pe_token_stride, void* q_pe, int64_t q_token_stride, int64_t q_head_stride,
+              int64_t num_heads, int64_t rope_dim, const void* weight, int weight_dtype, float eps,
+              const float* cos_table, const float* sin_table, int64_t table_rows, int64_t table_row_stride,
+              const int64_t* positions, int64_t num_tokens, void* latent, int64_t latent_token_stride,
+              const int64_t* slot_mapping, void* cache, int64_t num_slots, int64_t cache_slot_stride, int dtype,
+              void* stream) {
   if (num_tokens < 0 || kv_lora_rank <= 0 || num_heads < 0 || rope_dim <= 0 || rope_dim % 2 != 0) return EMBER_EINVAL;
   if (kv_lora_rank > (1 << 20) || rope_dim > 4096 || num_heads > (1 << 20)) return EMBER_EINVAL;
   if (table_rows < 0 || table_row_stride < rope_dim / 2) return EMBER_EINVAL;
   if (weight_dtype != dtype && weight_dtype != EMBER_F32) return EMBER_EINVAL;
   if (num_tokens == 0) return EMBER_OK;
   if (num_tokens > 0x1ffffffffLL) return EMBER_EINVAL;
-  if (c == nullptr || k_pe == nullptr || weight == nullptr || latent == nullptr || positions == nullptr ||
-      cos_table == nullptr || sin_table == nullptr || (num_heads > 0 && q_pe == nullptr))
+  if (c == nullptr || k_pe == nullptr || weight == nullptr || positions == nullptr || cos_table == nullptr ||
+      sin_table == nullptr || (num_heads > 0 && q_pe == nullptr))
     return EMBER_EINVAL;
-  if (latent_token_stride < kv_lora_rank + rope_dim) return EMBER_EINVAL;
-  MlaArgs a{c,          c_token_stride, kv_lora_rank, k_pe,      k_pe_token_stride, q_pe == nullptr ? latent : q_pe,
+  if (latent == nullptr && cache == nullptr) return EMBER_EINVAL;
+  if (latent != nullptr && latent_token_stride < kv_lora_rank + rope_dim) return EMBER_EINVAL;
+  if (cache != nullptr && (slot_mapping == nullptr || num_slots < 0 || cache_slot_stride < kv_lora_rank + rope_dim))
+    return EMBER_EINVAL;
+  MlaArgs a{c,          c_token_stride, kv_lora_rank, k_pe,      k_pe_token_stride,
+            q_pe == nullptr ? (latent != nullptr ? latent : cache) : q_pe,
             q_token_stride, q_head_stride, num_heads, rope_dim, weight,   eps,
             cos_table,  sin_table,      table_rows,   table_row_stride, positions, num_tokens,
             latent,     latent_token_stride, static_cast<hipStream_t>(stream), nullptr};
+  a.slots = slot_mapping;
+  a.cache = cache;
+  a.num_slots = num_slots;
+  a.css = cache_slot_stride;
   a.err = device_error_word();
   if (a.err == nullptr) return EMBER_ENODEV;
   const bool wf = weight_dtype == EMBER_F32 && dtype != EMBER_F32;
@@ -791,6 +836,38 @@ int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora
     case EMBER_BF16: return wf ? launch_mla_typed<__bf16, float>(a) : launch_mla_typed<__bf16, __bf16>(a);
     default: return EMBER_EINVAL;
   }
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora_rank, const void* k_pe,
+                          int64_t k_pe_token_stride, void* q_pe, int64_t q_token_stride, int64_t q_head_stride,
+                          int64_t num_heads, int64_t rope_dim, const void* weight, int weight_dtype, float eps,
+                          const float* cos_table, const float* sin_table, int64_t table_rows,
+                          int64_t table_row_stride, const int64_t* positions, int64_t num_tokens, void* latent,
+                          int64_t latent_token_stride, int dtype, void* stream) {
+  if (latent == nullptr) return EMBER_EINVAL;
+  return ember::mla_entry(c, c_token_stride, kv_lora_rank, k_pe, k_pe_token_stride, q_pe, q_token_stride,
+                          q_head_stride, num_heads, rope_dim, weight, weight_dtype, eps, cos_table, sin_table,
+                          table_rows, table_row_stride, positions, num_tokens, latent, latent_token_stride, nullptr,
+                          nullptr, 0, 0, dtype, stream);
+}
+
+int ember_mla_latent_rope_cache(const void* c, int64_t c_token_stride, int64_t kv_lora_rank, const void* k_pe,
+                                int64_t k_pe_token_stride, void* q_pe, int64_t q_token_stride, int64_t q_head_stride,
+                                int64_t num_heads, int64_t rope_dim, const void* weight, int weight_dtype, float eps,
+                                const float* cos_table, const float* sin_table, int64_t table_rows,
+                                int64_t table_row_stride, const int64_t* positions, int64_t num_tokens,
+                                void* latent, int64_t latent_token_stride, const int64_t* slot_mapping, void* cache,
+                                int64_t num_slots, int64_t cache_slot_stride, int dtype, void* stream) {
+  if (cache == nullptr) return EMBER_EINVAL;
+  return ember::mla_entry(c, c_token_stride, kv_lora_rank, k_pe, k_pe_token_stride, q_pe, q_token_stride,
+                          q_head_stride, num_heads, rope_dim, weight, weight_dtype, eps, cos_table, sin_table,
+                          table_rows, table_row_stride, positions, num_tokens, latent, latent_token_stride,
+                          slot_mapping, cache, num_slots, cache_slot_stride, dtype, stream);
 }
 
 int ember_rope_kv_cache(void* q, int64_t q_token_stride, int64_t q_head_stride, int64_t num_q_heads, void* k,

@@ -52,6 +52,7 @@ __all__ = [
     "embedding_torch", "qk_norm_rope_torch", "mla_latent_rope_torch",
     "kv_cache_write", "latent_cache_write", "kv_cache_write_hip", "latent_cache_write_hip",
     "kv_cache_write_torch", "latent_cache_write_torch", "rope_kv_cache", "rope_kv_cache_hip",
+    "mla_latent_rope_cache", "mla_latent_rope_cache_hip",
 ]
 
 
@@ -419,6 +420,52 @@ def rope_kv_cache_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: to
     return q, k
 
 
+def mla_latent_rope_cache_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, weight: torch.Tensor,
+                              eps: float, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                              slot_mapping: torch.Tensor, cache: torch.Tensor,
+                              return_latent: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """mla_latent_rope fused with PagedLatentCache.write (kv/cache.py:152-157): the latent
+    rows go straight to cache[slot] (and to a new [N, R + Dr] tensor when return_latent,
+    which the fresh-prefill attention reads). Returns (q_pe, latent or None)."""
+    _require_device("mla_latent_rope_cache", c, k_pe, q_pe, weight, cos, sin, positions, slot_mapping, cache)
+    n, r = c.shape
+    kp = k_pe.reshape(k_pe.shape[0], -1)
+    nh, dr = q_pe.shape[1], q_pe.shape[2]
+    if kp.shape != (n, dr) or q_pe.shape[0] != n:
+        raise ValueError("mla_latent_rope_cache: c [N, R], k_pe [N, Dr], q_pe [N, H, Dr] expected")
+    if c.stride(1) != 1 or kp.stride(1) != 1 or q_pe.stride(2) != 1 or dr % 2 != 0:
+        raise AssertionError("mla_latent_rope_cache: unit innermost stride and an even rope dim required")
+    if c.dtype != kp.dtype or c.dtype != q_pe.dtype or cache.dtype != c.dtype:
+        raise ValueError("mla_latent_rope_cache: c, k_pe, q_pe and the cache must share a dtype")
+    if weight.numel() != r or cache.shape[-1] != r + dr or cache.stride(-1) != 1:
+        raise ValueError("mla_latent_rope_cache: weight [R] and cache rows [R + Dr] expected")
+    if slot_mapping.numel() != n:
+        raise ValueError("mla_latent_rope_cache: one slot per token expected")
+    latent = torch.empty((n, r + dr), dtype=c.dtype, device=c.device) if return_latent else None
+    if n == 0:
+        return q_pe, latent
+    w, wtag = _weight_for(weight, c)
+    cos, sin, positions = _tables(cos, sin, positions, dr)
+    slots = (slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.long()).contiguous()
+    flat = cache.view(-1, r + dr)
+    idx = c.device.index
+    with torch.cuda.device(idx):
+        st = _lib.load().ember_mla_latent_rope_cache(
+            c.data_ptr(), c.stride(0), r, kp.data_ptr(), kp.stride(0), q_pe.data_ptr(), q_pe.stride(0),
+            q_pe.stride(1), nh, dr, w.data_ptr(), wtag, float(eps), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+            cos.stride(0), positions.data_ptr(), n, latent.data_ptr() if latent is not None else None,
+            latent.stride(0) if latent is not None else 0, slots.data_ptr(), flat.data_ptr(), flat.shape[0],
+            flat.stride(0), _lib.dtype_tag(c.dtype), torch._C._cuda_getCurrentRawStream(idx))
+    if st == 2:  # EMBER_EALIGN: the unfused pair
+        q_pe, lat = mla_latent_rope_hip(c, k_pe, q_pe, weight, eps, cos, sin, positions)
+        latent_cache_write_hip(lat, slots, cache)
+        return q_pe, lat if return_latent else None
+    _lib.check(st, "ember_mla_latent_rope_cache")
+    if _check_indices():
+        _raise_index_errors()
+    return q_pe, latent
+
+
 # ---- dispatch (ops.py:92-115 plus the fused additions) ----------------------------------
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -495,3 +542,15 @@ def rope_kv_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.
         q, k = rope_torch(q, k, cos, sin, positions)
     kv_cache_write_torch(k, v, slot_mapping, k_cache, v_cache)
     return q, k
+
+
+def mla_latent_rope_cache(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tensor, weight: torch.Tensor,
+                          eps: float, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor,
+                          slot_mapping: torch.Tensor, cache: torch.Tensor,
+                          return_latent: bool = True) -> tuple[torch.Tensor, torch.Tensor | None]:
+    if fused_enabled(c):
+        return mla_latent_rope_cache_hip(c, k_pe, q_pe, weight, eps, cos, sin, positions, slot_mapping, cache,
+                                         return_latent)
+    q_pe, latent = mla_latent_rope_torch(c, k_pe, q_pe, weight, eps, cos, sin, positions)
+    latent_cache_write_torch(latent, slot_mapping, cache)
+    return q_pe, latent if return_latent else None

@@ -36,6 +36,8 @@
  *                             emberserve/model/deepseek.py:124-133
  *   ember_kv_cache_write      PagedKVCache.write, emberserve/kv/cache.py:54-61
  *   ember_latent_cache_write  PagedLatentCache.write, emberserve/kv/cache.py:152-157
+ *   ember_mla_latent_rope_cache  ember_mla_latent_rope followed by PagedLatentCache.write
+ *                             (deepseek.py:124-133 then attn/mla_triton.py:235)
  *   ember_rope_kv_cache       rotary_emb (with the Qwen3 q/k norm when weights are given)
  *                             followed by PagedKVCache.write: qwen2.py:95-101 and the
  *                             backends' cache.write (attn/paged_triton.py:477)
@@ -181,6 +183,23 @@ int ember_latent_cache_write(const void* latent, int64_t latent_token_stride, in
                              const int64_t* slot_mapping, int64_t num_tokens,
                              void* cache, int64_t num_slots, int64_t cache_slot_stride,
                              int64_t elem_bytes, void* stream);
+
+/* ember_mla_latent_rope fused with the paged latent-cache write that follows it
+ * (PagedLatentCache.write): the latent rows are stored at cache[slot_mapping[t], :] (slot
+ * stride cache_slot_stride, slots outside [0, num_slots) skipped with EMBER_ERR_KV_SLOT)
+ * and, when latent != NULL, also to latent[t, :]. Needs 16-byte aligned operands;
+ * otherwise returns EMBER_EALIGN and does nothing. */
+int ember_mla_latent_rope_cache(const void* c, int64_t c_token_stride, int64_t kv_lora_rank,
+                                const void* k_pe, int64_t k_pe_token_stride,
+                                void* q_pe, int64_t q_token_stride, int64_t q_head_stride, int64_t num_heads,
+                                int64_t rope_dim,
+                                const void* weight, int weight_dtype, float eps,
+                                const float* cos_table, const float* sin_table,
+                                int64_t table_rows, int64_t table_row_stride,
+                                const int64_t* positions, int64_t num_tokens,
+                                void* latent, int64_t latent_token_stride,
+                                const int64_t* slot_mapping, void* cache, int64_t num_slots,
+                                int64_t cache_slot_stride, int dtype, void* stream);
 
 /* Rope (and, when q_weight != NULL, the Qwen3 per-head q/k RMSNorm before it) fused with
  * the paged KV-cache write that follows it: q and k are transformed in place exactly as by

@@ -748,3 +748,61 @@ def test_rope_kv_cache_unaligned_falls_back():
     assert_bitexact(qd, want_q, "q")
     assert_bitexact(kc, want_kc, "k cache")
     assert_bitexact(vc, want_vc, "v cache")
+
+
+@pytest.mark.parametrize("return_latent", [True, False])
+@pytest.mark.parametrize("in_model", [False, True])
+def test_mla_latent_rope_cache_fused(return_latent, in_model):
+    """MLA latent path with the latent rows written straight into the paged latent cache:
+    the cache rows equal mla_latent_rope's latent rows bit for bit, and match the oracle's
+    latent + PagedLatentCache.write."""
+    tokens, heads, nope, dr, rank, blocks, bs = 96, 16, 128, 64, 512, 16, 16
+    data, w, pos, qsize = _mla_case(tokens, in_model, seed=110)
+    cos, sin = _tables(dr, 8192, 5e4)
+    slots = torch.randperm(blocks * bs, generator=torch.Generator().manual_seed(111))[:tokens]
+
+    def views(q_buf, kv):
+        q = q_buf.view(tokens, heads, nope + dr)
+        return q[..., :nope], q[..., nope:], kv[:, :rank], kv[:, rank:]
+
+    if in_model:
+        _, q_pe, c, k_pe = views(data[:, :qsize], data[:, qsize:])
+        dev_buf = data.to(DEV)
+        _, q_pe_d, c_d, k_pe_d = views(dev_buf[:, :qsize], dev_buf[:, qsize:])
+    else:
+        q, kv_a = data
+        _, q_pe, c, k_pe = views(q, kv_a)
+        _, q_pe_d, c_d, k_pe_d = views(q.to(DEV), kv_a.to(DEV))
+    want_q_pe, want_lat = ref.mla_latent_rope(c, k_pe, q_pe, w, 1e-6, cos, sin, pos)
+    want_cache = torch.zeros(blocks, bs, rank + dr, dtype=torch.bfloat16)
+    ref.latent_cache_write(want_lat, slots, want_cache)
+    cache = torch.zeros(blocks, bs, rank + dr, dtype=torch.bfloat16, device=DEV)
+    got_q_pe, lat = ops.mla_latent_rope_cache_hip(c_d, k_pe_d, q_pe_d, w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV),
+                                                  pos.to(DEV), slots.to(DEV), cache, return_latent)
+    assert_bitexact(got_q_pe, want_q_pe, "q_pe")
+    rows = cache.view(-1, rank + dr)[slots.to(DEV)]
+    assert_ulp(rows[:, :rank], want_lat[:, :rank], 2, "cached latent c")
+    assert_bitexact(rows[:, rank:], want_lat[:, rank:], "cached latent k_pe")
+    untouched = torch.ones(blocks * bs, dtype=torch.bool)
+    untouched[slots] = False
+    assert not bool(cache.view(-1, rank + dr)[untouched.to(DEV)].any())
+    if return_latent:
+        assert_bitexact(lat, rows, "latent tensor == cached rows")
+    else:
+        assert lat is None
+
+
+def test_mla_latent_rope_cache_unaligned_falls_back():
+    kv_a, q, w, pos = gen.mla_inputs(6, 2, 8, 16, 100, 64, torch.bfloat16, seed=112)  # rank 100: not 16-B rows
+    cos, sin = _tables(16, 64, 1e4)
+    slots = torch.tensor([3, 9, 0, 15, 4, 7])
+    qv = q.view(6, 2, 24)
+    want_q_pe, want_lat = ref.mla_latent_rope(kv_a[:, :100], kv_a[:, 100:], qv[..., 8:], w, 1e-6, cos, sin, pos)
+    want_cache = torch.zeros(2, 8, 116, dtype=torch.bfloat16)
+    ref.latent_cache_write(want_lat, slots, want_cache)
+    kd, qd = kv_a.to(DEV), q.to(DEV)
+    cache = torch.zeros(2, 8, 116, dtype=torch.bfloat16, device=DEV)
+    got_q_pe, lat = ops.mla_latent_rope_cache_hip(kd[:, :100], kd[:, 100:], qd[..., 8:], w.to(DEV), 1e-6, cos.to(DEV),
+                                                  sin.to(DEV), pos.to(DEV), slots.to(DEV), cache)
+    assert_bitexact(got_q_pe, want_q_pe, "q_pe")
+    assert_ulp(cache, want_cache, 2, "cache")
