@@ -76,10 +76,15 @@ def _raise_index_errors() -> None:
         raise IndexError("emberserve_amd.kv_cache_write: slot out of range of the cache")
 
 
-def _launch(what: str, fn, device: torch.device, *args) -> None:
+_EALIGN = 2  # EMBER_EALIGN: a fused entry point refused misaligned operands, nothing ran
+
+
+def _launch(what: str, fn, device: torch.device, *args, allow_unaligned: bool = False) -> bool:
     """Calls C-ABI entry point `fn(*args, stream)` with `device` current and torch's current
     stream on it (the capture stream while a torch.cuda.graph records), raising on a
-    non-zero status. Uses torch's raw-handle accessors: this is on every op's hot path."""
+    non-zero status. With allow_unaligned, EMBER_EALIGN is returned as False (the caller
+    then runs the unfused ops) instead of raising. Uses torch's raw-handle accessors: this
+    is on every op's hot path."""
     idx = device.index
     cur = torch._C._cuda_getDevice()
     if idx is None or idx == cur:
@@ -87,8 +92,11 @@ def _launch(what: str, fn, device: torch.device, *args) -> None:
     else:
         with torch.cuda.device(idx):
             st = fn(*args, torch._C._cuda_getCurrentRawStream(idx))
+    if st == _EALIGN and allow_unaligned:
+        return False
     if st != 0:
         _lib.check(st, what)
+    return True
 
 
 def _require_device(what: str, *tensors: torch.Tensor) -> None:
@@ -398,23 +406,20 @@ def rope_kv_cache_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: to
         if ktag != wtag:
             qw, kw, wtag = qw.float(), kw.float(), _lib.F32
         qw_ptr, kw_ptr = qw.data_ptr(), kw.data_ptr()
-    lib = _lib.load()
-    idx = q.device.index
-    with torch.cuda.device(idx):
-        st = lib.ember_rope_kv_cache(
-            q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0), k.stride(1), hk, v.data_ptr(),
-            v.stride(0), v.stride(1), d, qw_ptr, kw_ptr, wtag, float(eps), cos.data_ptr(), sin.data_ptr(),
-            cos.shape[0], cos.stride(0), positions.data_ptr(), slots.data_ptr(), n, k_cache.data_ptr(),
-            v_cache.data_ptr(), kc.shape[0], kc.stride(0), kc.stride(1), _lib.dtype_tag(q.dtype),
-            torch._C._cuda_getCurrentRawStream(idx))
-    if st == 2:  # EMBER_EALIGN: the unfused pair
+    fused = _launch(
+        "ember_rope_kv_cache", _lib.load().ember_rope_kv_cache, q.device,
+        q.data_ptr(), q.stride(0), q.stride(1), h, k.data_ptr(), k.stride(0), k.stride(1), hk, v.data_ptr(),
+        v.stride(0), v.stride(1), d, qw_ptr, kw_ptr, wtag, float(eps), cos.data_ptr(), sin.data_ptr(),
+        cos.shape[0], cos.stride(0), positions.data_ptr(), slots.data_ptr(), n, k_cache.data_ptr(),
+        v_cache.data_ptr(), kc.shape[0], kc.stride(0), kc.stride(1), _lib.dtype_tag(q.dtype),
+        allow_unaligned=True)
+    if not fused:  # misaligned operands: the unfused pair
         if norm:
             qk_norm_rope_hip(q, k, q_weight, k_weight, eps, cos, sin, positions)
         else:
             rope_hip(q, k, cos, sin, positions)
         kv_cache_write_hip(k, v, slots, k_cache, v_cache)
         return q, k
-    _lib.check(st, "ember_rope_kv_cache")
     if _check_indices():
         _raise_index_errors()
     return q, k
@@ -448,19 +453,17 @@ def mla_latent_rope_cache_hip(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.T
     cos, sin, positions = _tables(cos, sin, positions, dr)
     slots = (slot_mapping if slot_mapping.dtype == torch.int64 else slot_mapping.long()).contiguous()
     flat = cache.view(-1, r + dr)
-    idx = c.device.index
-    with torch.cuda.device(idx):
-        st = _lib.load().ember_mla_latent_rope_cache(
-            c.data_ptr(), c.stride(0), r, kp.data_ptr(), kp.stride(0), q_pe.data_ptr(), q_pe.stride(0),
-            q_pe.stride(1), nh, dr, w.data_ptr(), wtag, float(eps), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
-            cos.stride(0), positions.data_ptr(), n, latent.data_ptr() if latent is not None else None,
-            latent.stride(0) if latent is not None else 0, slots.data_ptr(), flat.data_ptr(), flat.shape[0],
-            flat.stride(0), _lib.dtype_tag(c.dtype), torch._C._cuda_getCurrentRawStream(idx))
-    if st == 2:  # EMBER_EALIGN: the unfused pair
+    fused = _launch(
+        "ember_mla_latent_rope_cache", _lib.load().ember_mla_latent_rope_cache, c.device,
+        c.data_ptr(), c.stride(0), r, kp.data_ptr(), kp.stride(0), q_pe.data_ptr(), q_pe.stride(0),
+        q_pe.stride(1), nh, dr, w.data_ptr(), wtag, float(eps), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        cos.stride(0), positions.data_ptr(), n, latent.data_ptr() if latent is not None else None,
+        latent.stride(0) if latent is not None else 0, slots.data_ptr(), flat.data_ptr(), flat.shape[0],
+        flat.stride(0), _lib.dtype_tag(c.dtype), allow_unaligned=True)
+    if not fused:  # misaligned operands: the unfused pair
         q_pe, lat = mla_latent_rope_hip(c, k_pe, q_pe, weight, eps, cos, sin, positions)
         latent_cache_write_hip(lat, slots, cache)
         return q_pe, lat if return_latent else None
-    _lib.check(st, "ember_mla_latent_rope_cache")
     if _check_indices():
         _raise_index_errors()
     return q_pe, latent
