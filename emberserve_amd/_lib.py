@@ -13,12 +13,15 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
 ERR_ROPE_POS = 2
 ERR_KV_SLOT = 4
+ERR_DECODE_CTX = 8
+ERR_BLOCK_ID = 16
+DECODE_FP32 = 1
 
 _DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -48,10 +51,16 @@ SIGNATURES: dict[str, list] = {
                             _p, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _p],
     "ember_mla_latent_rope_cache": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _f32,
                                     _p, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i32, _p],
+    "ember_paged_decode_workspace_bytes": [_i64, _i64, _i64, _i64],
+    "ember_paged_decode": [_p, _i64, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                           _i64, _i32, _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _i32, _p, _i64, _p, _i64,
+                           _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],
 }
+
+_RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspace_bytes": ctypes.c_int64}
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:
@@ -72,7 +81,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == "ember_status_string" else ctypes.c_int
+            fn.restype = _RESTYPE.get(name, ctypes.c_int)
         got = lib.ember_abi_version()
         if got != ABI_VERSION:
             raise RuntimeError(f"emberserve_amd: {p} has ABI version {got}, expected {ABI_VERSION}; rebuild it")

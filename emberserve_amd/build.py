@@ -23,9 +23,12 @@ ARCH = "gfx950"
 # -ffp-contract=off: a*b+c stays two rounded operations, as in the reference's separate
 # element-wise tensor ops (the rope and norm parity depends on it).
 # -packed-fp32-ops: keep hipcc from forming packed fp32 instructions.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in ordinary VGPRs, so the decode kernel's
+# online-softmax rescale of its accumulators needs no accvgpr copies.
 HIP_FLAGS = [
     "-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 

@@ -34,7 +34,7 @@ __host__ uint32_t* device_error_word() {
 
 extern "C" {
 
-int ember_abi_version(void) { return 4; }
+int ember_abi_version(void) { return 5; }
 
 const char* ember_status_string(int status) {
   switch (status) {

@@ -41,6 +41,10 @@
  *   ember_rope_kv_cache       rotary_emb (with the Qwen3 q/k norm when weights are given)
  *                             followed by PagedKVCache.write: qwen2.py:95-101 and the
  *                             backends' cache.write (attn/paged_triton.py:477)
+ *   ember_paged_decode        paged_attention_decode, emberserve/attn/paged_triton.py:323-399
+ *                             (kernels :95-209; fp32 definition attn/paged_torch.py:87-98)
+ *   ember_paged_decode_workspace_bytes  the split-K scratch size (_Scratch,
+ *                             attn/paged_triton.py:293-310)
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
@@ -67,6 +71,8 @@ extern "C" {
 #define EMBER_ERR_EMBED_ID 1u   /* a token id outside [0, vocab) */
 #define EMBER_ERR_ROPE_POS 2u   /* a position outside [0, table_rows) */
 #define EMBER_ERR_KV_SLOT 4u    /* a cache slot outside [0, num_slots) */
+#define EMBER_ERR_DECODE_CTX 8u /* a context length outside [0, max_blocks * block_size] */
+#define EMBER_ERR_BLOCK_ID 16u  /* a block-table entry outside [0, num_blocks) */
 
 /* ABI version, bumped when an entry point is added or its signature changes. */
 int ember_abi_version(void);
@@ -219,6 +225,44 @@ int ember_rope_kv_cache(void* q, int64_t q_token_stride, int64_t q_head_stride, 
                         void* k_cache, void* v_cache, int64_t num_slots,
                         int64_t cache_slot_stride, int64_t cache_head_stride,
                         int dtype, void* stream);
+
+/* Bytes of workspace ember_paged_decode needs for num_splits > 1 (0 for one split), -1 for
+ * invalid arguments: fp32 partials [splits][seqs][heads][head_dim + 2] and one uint32
+ * arrival counter per (sequence, head). */
+int64_t ember_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t head_dim,
+                                           int64_t num_splits);
+
+/* One-query-per-sequence attention over a paged KV cache (paged_attention_decode):
+ *   out[b, h, :] = softmax_j(scale * q[b, h] . k[b, j]) @ v[b, j],  j < context_lens[b],
+ * key j of sequence b at block block_tables[b, j / block_size], slot j % block_size, KV head
+ * h / (num_heads / num_kv_heads). q and out are [num_seqs, num_heads, head_dim] of q_dtype
+ * (unit stride on the last dim); the caches are [num_blocks, block_size, num_kv_heads,
+ * head_dim] of cache_dtype with the given element strides; block_tables int32
+ * [num_seqs, >= max_blocks] (row stride block_table_stride); context_lens int32 [num_seqs].
+ * block_size must be a multiple of 16 and head_dim <= 256. With num_splits > 1 each
+ * sequence's context is cut into num_splits key ranges whose partial results are merged by
+ * the last split to finish (or a second kernel) through `workspace`
+ * (ember_paged_decode_workspace_bytes bytes, 16-byte aligned, zero-filled before its first
+ * use; every call leaves it ready for the next, and calls that overlap on one workspace
+ * race); the split count changes rounding only, never which keys are seen.
+ * fp16/bf16 q and cache of the same dtype with head_dim 64 or 128 and 16-byte aligned
+ * operands run on MFMA with the reference's tl.dot numerics (fp32 scores, probabilities
+ * rounded to the cache dtype for P.V); every other case computes in fp32. Context lengths
+ * outside [0, max_blocks * block_size] are clamped (EMBER_ERR_DECODE_CTX); block ids outside
+ * [0, num_blocks) read block 0 (EMBER_ERR_BLOCK_ID). A zero context yields NaN rows, as the
+ * reference kernel's 0/0 does. flags: 0, or EMBER_DECODE_FP32 to compute in fp32 whatever
+ * the dtypes (the reference's "sum" variant). */
+#define EMBER_DECODE_FP32 1
+int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
+                       const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
+                       int64_t num_kv_heads, int64_t head_dim,
+                       int64_t k_block_stride, int64_t k_slot_stride, int64_t k_head_stride,
+                       int64_t v_block_stride, int64_t v_slot_stride, int64_t v_head_stride,
+                       int cache_dtype,
+                       const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                       const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                       int64_t num_splits, int flags, void* workspace, int64_t workspace_bytes,
+                       void* out, int64_t out_seq_stride, int64_t out_head_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -70,3 +70,29 @@ def mla_inputs(tokens: int, heads: int, nope: int, rope_dim: int, rank: int, max
     w = normal((rank,), dtype, seed + 2, mean=1.0, std=0.1)
     pos = uniform_ints(tokens, max_pos, seed + 3)
     return kv_a, q, w, pos
+
+
+def decode_inputs(ctx_lens, hq: int, hkv: int, d: int, block: int, dtype, seed: int = 0,
+                  spare_blocks: int = 1, table_width: int | None = None):
+    """A paged decode step in the shape of the reference's decode tests and kernel bench
+    (tests/test_paged_triton_gpu.py:50-87, scripts/bench_kernels.py:55-80): every cache
+    block holds N(0, 1) K/V (stale blocks hold real data, so a wrong table read shows), each
+    sequence's blocks are a random permutation of the pool (scrambled, non-contiguous
+    tables), q ~ N(0, 1). Table padding entries are valid block ids (0), as the backend
+    passes them (attn/paged_flash.py:91-96). Returns (q, k_cache, v_cache, block_tables
+    int32, context_lens int32)."""
+    ctx = [int(c) for c in ctx_lens]
+    g = gen(seed)
+    per = [-(-c // block) for c in ctx]
+    num_blocks = sum(per) + spare_blocks
+    width = max(1, max(per) if per else 1) if table_width is None else table_width
+    k_cache = torch.randn(num_blocks, block, hkv, d, generator=g).to(dtype)
+    v_cache = torch.randn(num_blocks, block, hkv, d, generator=g).to(dtype)
+    perm = torch.randperm(num_blocks, generator=g).tolist()
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(per):
+        tables[i, :n] = torch.tensor(perm[at:at + n], dtype=torch.int32)
+        at += n
+    q = torch.randn(len(ctx), hq, d, generator=g).to(dtype)
+    return q, k_cache, v_cache, tables, torch.tensor(ctx, dtype=torch.int32)

@@ -23,6 +23,11 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                columns bit-exact.
   kv_cache_write, latent_cache_write  an explicit per-token loop of slice assignments
                                (slot by slot), bit-exact; untouched slots stay untouched.
+  gather_batch, paged_decode   float64 brute force over the block table, key by key
+                               (math.exp, Python sums); one key gives its V row; equal
+                               keys give the mean of V; relocating blocks leaves the result
+                               unchanged; GQA maps head h to KV head h // G; the per-sequence
+                               causal_softmax_attention formulation (attn/base.py:105-128).
 No function is left unpinned.
 """
 
@@ -148,3 +153,55 @@ def latent_cache_write(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: 
     [num_blocks, block_size, latent_dim]."""
     slots = slot_mapping.to(device=cache.device, dtype=torch.long)
     cache.view(-1, latent.shape[-1]).index_copy_(0, slots, latent.to(cache.dtype))
+
+
+def gather_batch(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 context_lens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """emberserve/kv/cache.py:81-107 (PagedKVCache.gather_batch) for one layer's caches
+    [num_blocks, block_size, Hkv, D]: padded K/V [B, max_ctx, Hkv, D] and the validity mask
+    [B, max_ctx]; negative table entries are clamped to 0 as there."""
+    bs = k_cache.shape[1]
+    ctx = context_lens.to(dtype=torch.long)
+    max_ctx = int(ctx.max())
+    nb = -(-max_ctx // bs)
+    idx = block_tables[:, :nb].to(dtype=torch.long).clamp_min(0)
+    batch = idx.shape[0]
+
+    def one(store: torch.Tensor) -> torch.Tensor:
+        blocks = store[idx]
+        return blocks.reshape(batch, nb * bs, store.shape[2], store.shape[3])[:, :max_ctx]
+
+    valid = torch.arange(max_ctx)[None, :] < ctx[:, None]
+    return one(k_cache), one(v_cache), valid
+
+
+def paged_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                 block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """emberserve/attn/paged_torch.py:87-98 (PagedTorchAttentionBackend._decode), the fp32
+    definition every decode kernel of the reference is tested against: GQA-expanded fp32
+    K/V, scores * scale, masked softmax, P.V; the result in q.dtype."""
+    k, v, valid = gather_batch(k_cache, v_cache, block_tables, context_lens)
+    groups = q.shape[1] // k_cache.shape[2]
+    kf = k.float().repeat_interleave(groups, dim=2)
+    vf = v.float().repeat_interleave(groups, dim=2)
+    scores = torch.einsum("bhd,bkhd->bhk", q.float(), kf) * scale
+    scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    out = torch.einsum("bhk,bkhd->bhd", probs, vf)
+    return out.to(q.dtype)
+
+
+def paged_decode_prob_mass(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           block_tables: torch.Tensor, context_lens: torch.Tensor,
+                           scale: float) -> torch.Tensor:
+    """sum_j p_j |v_j| per output element (fp32, [B, H, D]), the same softmax as
+    paged_decode: the scale of the error that rounding the probabilities to the cache dtype
+    before P.V (the reference's tl.dot variant, attn/paged_triton.py:163-167) can add."""
+    k, v, valid = gather_batch(k_cache, v_cache, block_tables, context_lens)
+    groups = q.shape[1] // k_cache.shape[2]
+    kf = k.float().repeat_interleave(groups, dim=2)
+    vf = v.float().repeat_interleave(groups, dim=2)
+    scores = torch.einsum("bhd,bkhd->bhk", q.float(), kf) * scale
+    scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    return torch.einsum("bhk,bkhd->bhd", probs, vf.abs())

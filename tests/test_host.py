@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from emberserve_amd import _lib, layers, ops, rope
+from oracle import inputs as gen
 from oracle import ref_ops as ref
 from tests.helpers import assert_bitexact
 
@@ -203,3 +204,49 @@ def test_silu_and_mul_rejects_odd_width():
     if torch.cuda.is_available():
         with pytest.raises(ValueError):
             ops.silu_and_mul_hip(torch.randn(2, 7, device="cuda"))
+
+
+# ---- paged decode attention (host side) ----------------------------------------------------
+def test_paged_decode_cpu_path_matches_oracle_and_asserts_like_the_reference():
+    from emberserve_amd.paged_decode import paged_attention_decode
+    q, kc, vc, bt, cl = gen.decode_inputs([5, 19, 40], 4, 2, 64, 16, torch.float32, seed=0)
+    got = paged_attention_decode(q, kc, vc, bt, cl, 64 ** -0.5, num_splits=1)
+    torch.testing.assert_close(got, ref.paged_decode(q, kc, vc, bt, cl, 64 ** -0.5), rtol=0, atol=1e-6)
+    bad = torch.randn(2, 8, 1, 64)  # block_size 8: test_paged_triton.py:272-277
+    with pytest.raises(AssertionError, match="block_size"):
+        paged_attention_decode(torch.randn(1, 2, 64), bad, bad, torch.zeros(1, 1, dtype=torch.int32),
+                               torch.ones(1, dtype=torch.int32), 1.0)
+    with pytest.raises(AssertionError, match="head_dim"):
+        kc48 = torch.randn(2, 16, 1, 48)
+        paged_attention_decode(torch.randn(1, 2, 48), kc48, kc48, torch.zeros(1, 1, dtype=torch.int32),
+                               torch.ones(1, dtype=torch.int32), 1.0)
+
+
+def test_paged_decode_abi_rejects_bad_arguments_before_any_device_call():
+    lib = _lib.load()
+    assert lib.ember_paged_decode_workspace_bytes(2, 4, 64, 1) == 0
+    assert lib.ember_paged_decode_workspace_bytes(2, 4, 64, 3) == 3 * 2 * 4 * 66 * 4 + 32
+    assert lib.ember_paged_decode_workspace_bytes(2, 4, 64, 0) == -1
+    base = dict(block_size=16, flags=0, heads=4, kv=2, d=64, splits=1)
+
+    def call(block_size, flags, heads, kv, d, splits):
+        return lib.ember_paged_decode(None, 0, 0, 1, None, None, 4, block_size, kv, d, 0, 0, 0, 0, 0, 0, 1,
+                                      None, 0, 1, None, 1, heads, 1.0, splits, flags, None, 0, None, 0, 0, None)
+    for bad in (dict(block_size=8), dict(flags=2), dict(heads=5), dict(d=300), dict(splits=0)):
+        assert call(**{**base, **bad}) == 1, bad
+    assert call(**base) == 1  # null pointers
+
+
+def test_paged_decode_default_splits_follow_the_grid_rule(monkeypatch):
+    from emberserve_amd import paged_decode as pd
+    monkeypatch.delenv("EMBERSERVE_TRITON_SPLITS", raising=False)
+    monkeypatch.setattr(pd, "num_sms", lambda device: 256)
+    dev = torch.device("cpu")
+    assert pd.default_num_splits(128, 8, 2048, dev, 32, 128) == 1      # 1024 programs
+    assert pd.default_num_splits(8, 8, 8192, dev, 32, 128) == 4        # 64 programs -> 256
+    assert pd.default_num_splits(128, 2, 8192, dev, 14, 64) == 2       # D=64: 2 per CU
+    assert pd.default_num_splits(1, 8, 8192, dev, 32, 128) == 32       # capped at MAX_SPLITS
+    assert pd.default_num_splits(1, 8, 512, dev, 32, 128) == 2         # >= 256 keys per split
+    assert pd.default_num_splits(4, 2, 100000, dev, 40, 64) == 32      # 20 heads/kv: 2 chunks
+    monkeypatch.setenv("EMBERSERVE_TRITON_SPLITS", "3")
+    assert pd.default_num_splits(128, 8, 2048, dev, 32, 128) == 3

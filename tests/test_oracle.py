@@ -316,3 +316,93 @@ def test_latent_cache_write_matches_slot_loop():
     for t in range(n):
         want[int(slots[t])] = lat[t]
     assert_bitexact(cache.view(-1, dim), want)
+
+
+# ---- paged decode attention --------------------------------------------------------------
+def _decode_brute_force(q, kc, vc, bt, ctx, scale):
+    """Key-by-key float64 softmax over the block table with Python sums and math.exp."""
+    B, H, D = q.shape
+    hkv = kc.shape[2]
+    bs = kc.shape[1]
+    G = H // hkv
+    out = np.zeros((B, H, D))
+    qd, kd, vd = q.double().numpy(), kc.double().numpy(), vc.double().numpy()
+    for b in range(B):
+        for h in range(H):
+            kvh = h // G
+            rows = [(int(bt[b, j // bs]), j % bs) for j in range(int(ctx[b]))]
+            s = [scale * sum(qd[b, h, e] * kd[blk, sl, kvh, e] for e in range(D)) for blk, sl in rows]
+            mx = max(s)
+            w = [math.exp(x - mx) for x in s]
+            tot = sum(w)
+            for e in range(D):
+                out[b, h, e] = sum(wj * vd[blk, sl, kvh, e] for wj, (blk, sl) in zip(w, rows)) / tot
+    return out
+
+
+def test_paged_decode_matches_brute_force():
+    q, kc, vc, bt, ctx = gen.decode_inputs([5, 19, 40], 4, 2, 8, 16, torch.float32, seed=3)
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 8 ** -0.5)
+    bf = _decode_brute_force(q, kc, vc, bt, ctx, 8 ** -0.5)
+    np.testing.assert_allclose(out.double().numpy(), bf, rtol=0, atol=2e-6)
+
+
+def test_paged_decode_single_key_returns_its_value_row():
+    q, kc, vc, bt, ctx = gen.decode_inputs([1, 1], 6, 3, 16, 16, torch.float32, seed=4)
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 0.25)
+    for b in range(2):
+        blk = int(bt[b, 0])
+        expect = vc[blk, 0].repeat_interleave(2, dim=0)  # head h -> KV head h // 2
+        assert torch.equal(out[b], expect)
+
+
+def test_paged_decode_equal_keys_average_the_values():
+    q, kc, vc, bt, ctx = gen.decode_inputs([37], 2, 1, 16, 16, torch.float32, seed=5)
+    kc[:] = kc[0, 0]  # every key identical -> uniform attention
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 0.3)
+    k, v, _ = ref.gather_batch(kc, vc, bt, ctx)
+    expect = v[0, :37, 0].double().mean(0)
+    for h in range(2):
+        np.testing.assert_allclose(out[0, h].double().numpy(), expect.numpy(), rtol=0, atol=1e-6)
+
+
+def test_paged_decode_is_invariant_to_block_relocation():
+    q, kc, vc, bt, ctx = gen.decode_inputs([23, 48], 4, 2, 8, 16, torch.float32, seed=6, spare_blocks=3)
+    base = ref.paged_decode(q, kc, vc, bt, ctx, 0.35)
+    perm = torch.randperm(kc.shape[0], generator=gen.gen(9))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    kc2, vc2 = kc[perm], vc[perm]  # block p of the new pool is old block perm[p]
+    bt2 = inv[bt.long()].to(torch.int32)
+    assert torch.equal(ref.paged_decode(q, kc2, vc2, bt2, ctx, 0.35), base)
+
+
+def test_paged_decode_gqa_maps_head_to_kv_head_group():
+    q, kc, vc, bt, ctx = gen.decode_inputs([30], 6, 2, 8, 16, torch.float32, seed=7)
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 0.35)
+    for h in range(6):  # the same head against a one-KV-head cache holding KV head h // 3
+        one = ref.paged_decode(q[:, h:h + 1], kc[:, :, h // 3:h // 3 + 1], vc[:, :, h // 3:h // 3 + 1],
+                               bt, ctx, 0.35)
+        torch.testing.assert_close(out[:, h:h + 1], one, rtol=0, atol=1e-6)
+
+
+def test_paged_decode_equals_per_sequence_causal_attention():
+    """attn/base.py:105-128 with Tq = 1 (the last key is the query's own position) over
+    each sequence's gathered context: the formulation the reference tests decode against."""
+    q, kc, vc, bt, ctx = gen.decode_inputs([17, 49, 1], 14, 2, 64, 16, torch.float32, seed=8)
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 64 ** -0.5)
+    k, v, _ = ref.gather_batch(kc, vc, bt, ctx)
+    for b, n in enumerate(ctx.tolist()):
+        kk = k[b, :n].float().repeat_interleave(7, dim=1).transpose(0, 1)  # [H, n, D]
+        vv = v[b, :n].float().repeat_interleave(7, dim=1).transpose(0, 1)
+        sc = torch.matmul(q[b].float()[:, None, :], kk.transpose(-1, -2)) / 8.0
+        o = torch.matmul(torch.softmax(sc, dim=-1), vv)[:, 0]
+        torch.testing.assert_close(out[b], o, rtol=0, atol=2e-6)
+
+
+def test_paged_decode_prob_mass_bounds_the_output():
+    q, kc, vc, bt, ctx = gen.decode_inputs([40, 3], 4, 2, 16, 16, torch.float32, seed=10)
+    out = ref.paged_decode(q, kc, vc, bt, ctx, 0.25)
+    mass = ref.paged_decode_prob_mass(q, kc, vc, bt, ctx, 0.25)
+    assert bool((out.abs() <= mass + 1e-6).all())
+    assert bool((mass <= vc.abs().amax() + 1e-6).all())
