@@ -111,7 +111,13 @@ def _cpu_factories():
         k, v, slots, kc, vc = _cpu_inputs(("kv", t), build)
         return lambda: ref.kv_cache_write(k, v, slots, kc, vc)
 
-    return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla, kv=kv)
+    def decode(b, ctx, hq, hkv, d, dtype):
+        q, kc, vc, bt, cl = _cpu_inputs(("decode", b, ctx, hq, hkv, d, dtype),
+                                        lambda: gen.decode_inputs([ctx] * b, hq, hkv, d, 16, dtype, seed=1))
+        return lambda: ref.paged_decode(q, kc, vc, bt, cl, d ** -0.5)
+
+    return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla, kv=kv,
+                decode=decode)
 
 
 def _cpu_time_row(fn, budget_s):
@@ -269,6 +275,26 @@ def _ops(torch, ops, tables):
                       lambda a: ops.mla_latent_rope_cache_hip(a[0], a[1], a[2], a[3], 1e-6, cos, sin, a[4], a[5],
                                                               a[6]), t * (576 * 3 + 3072) * 2))
 
+    def decode(cfg, b, ctx, hq, hkv, d, dtype, label, cpu=True):
+        from emberserve_amd.paged_decode import paged_attention_decode
+        bs = 16
+        per = ctx // bs
+        nblk = b * per + 1
+        e = 2
+
+        def make(i):
+            kc = randn((nblk, bs, hkv, d), dtype, 210 + i)
+            vc = randn((nblk, bs, hkv, d), dtype, 220 + i)
+            g.manual_seed(200 + i)  # scrambled block tables (bench_kernels.py:55-80)
+            bt = torch.randperm(nblk, generator=g, device=dev)[: b * per].to(torch.int32).view(b, per)
+            return (randn((b, hq, d), dtype, 230 + i), kc, vc, bt,
+                    torch.full((b,), ctx, dtype=torch.int32, device=dev))
+        kv_bytes = b * ctx * hkv * d * 2 * e
+        nbytes = kv_bytes + 2 * b * hq * d * e + 4 * b * (per + 1)  # K+V, q + out, tables + lengths
+        out.append(Op("paged_decode", cfg, f"{label}: B={b} ctx={ctx} {hq}q/{hkv}kv x{d} {str(dtype)[6:]} block 16",
+                      nbytes, make, lambda a: paged_attention_decode(a[0], a[1], a[2], a[3], a[4], d ** -0.5),
+                      kv_bytes, cpu=("decode", (b, ctx, hq, hkv, d, dtype)) if cpu else None))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -290,6 +316,13 @@ def _ops(torch, ops, tables):
     latent_write("kv", 8192)
     mla_cache("kv", 8192)
     silu("extra", 8192, inter=12288, dtype=bf, label="silu_and_mul")  # Qwen3-8B MLP
+    # Paged decode attention (attn/paged_triton.py:323-399) at the reference's kernel-bench
+    # geometry (scripts/bench_kernels.py: Qwen2.5-0.5B, 14q/2kv x64 fp16, ctx 2048) and at
+    # Qwen3-8B's (32q/8kv x128 bf16).
+    for b in (1, 8, 32, 128):
+        decode("decode", b, 2048, 14, 2, 64, f16, "qwen2.5-0.5b")
+    decode("decode", 8, 8192, 32, 8, 128, bf, "qwen3-8b")
+    decode("decode", 64, 4096, 32, 8, 128, bf, "qwen3-8b", cpu=False)
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
     # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the

@@ -64,7 +64,6 @@ struct Mfma<__bf16> {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 32;      // keys per tile (one P.V MFMA deep)
-constexpr int kWaves = 4;      // waves per workgroup of the MFMA kernel
 constexpr int kVtPad = 8;      // elements of padding per Vt row (keeps 16-byte alignment)
 
 struct DecodeArgs {
@@ -166,22 +165,31 @@ __device__ __forceinline__ void split_range(int ctx, int splits, int split, int&
 #ifndef EMBER_DECODE_PF128
 #define EMBER_DECODE_PF128 1
 #endif
+#ifndef EMBER_DECODE_NW64
+#define EMBER_DECODE_NW64 8
+#endif
+#ifndef EMBER_DECODE_NW128
+#define EMBER_DECODE_NW128 4
+#endif
+// Waves per workgroup (each streams its own tiles of the workgroup's key range).
+constexpr int kWaves64 = EMBER_DECODE_NW64;
+constexpr int kWaves128 = EMBER_DECODE_NW128;
 
-template <typename T, int D, int KT, bool PF>
-__global__ void __launch_bounds__(kWaves * kWave)
+template <typename T, int D, int KT, bool PF, int NW>
+__global__ void __launch_bounds__(NW * kWave)
 k_decode_mfma(DecodeArgs a) {
   using M = Mfma<T>;
   using V8 = typename M::v8;
   constexpr int NP = D / 32;       // 16-byte packs per lane per key row (= QK MFMAs per half)
   constexpr int NDT = D / 16;      // d tiles of P.V
   constexpr int VS = D + kVtPad;   // LDS row stride of the V tile (elements)
-  constexpr int CH = KT * kWaves;  // tiles between two chunks of one wave
+  constexpr int CH = KT * NW;      // tiles between two chunks of one wave
   struct Combine {
-    float m[kWaves][16];
-    float l[kWaves][16];
-    float o[kWaves][16][D + 4];
+    float m[NW][16];
+    float l[NW][16];
+    float o[NW][16][D + 4];
   };
-  constexpr int kVtBytes = kWaves * KT * kTile * VS * int(sizeof(T));
+  constexpr int kVtBytes = NW * KT * kTile * VS * int(sizeof(T));
   constexpr int kLdsBytes = kVtBytes > int(sizeof(Combine)) ? kVtBytes : int(sizeof(Combine));
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
 
@@ -368,9 +376,10 @@ k_decode_mfma(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) cb.o[w][n][16 * dt + 4 * g + i] = o[dt][i];
   __syncthreads();
 
-  constexpr int PER = D / 16;  // d values per thread: 256 threads = 16 heads x 16 parts
-  const int hh = threadIdx.x >> 4;
-  const int d0 = (threadIdx.x & 15) * PER;
+  constexpr int PARTS = NW * kWave / 16;  // threads per head in the merge
+  constexpr int PER = D / PARTS;           // d values per thread
+  const int hh = threadIdx.x / PARTS;
+  const int d0 = (threadIdx.x % PARTS) * PER;
   const bool mine = hh < nhc;
   const int head = head0 + hh;
   float mx = -INFINITY;
@@ -379,14 +388,14 @@ k_decode_mfma(DecodeArgs a) {
 #pragma unroll
   for (int e = 0; e < PER; ++e) acc[e] = 0.f;
   if (mine) {
-    float mw[kWaves];
+    float mw[NW];
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) {
+    for (int v = 0; v < NW; ++v) {
       mw[v] = cb.m[v][hh];
       mx = fmaxf(mx, mw[v]);
     }
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) {
+    for (int v = 0; v < NW; ++v) {
       const float wt = mw[v] == -INFINITY ? 0.f : exp2_fast(mw[v] - mx);
       L += wt * cb.l[v][hh];
 #pragma unroll
@@ -414,7 +423,7 @@ k_decode_mfma(DecodeArgs a) {
   const int64_t stride = int64_t(a.nseq) * a.nh;
   const int64_t row = int64_t(split) * stride + int64_t(b) * a.nh + head;
   if (mine) {
-    if ((threadIdx.x & 15) == 0) {
+    if (threadIdx.x % PARTS == 0) {
       store_agent(a.part_m + row, mx);
       store_agent(a.part_l + row, L);
     }
@@ -591,9 +600,11 @@ int launch_any_q(int cdt, const DecodeArgs& a, dim3 grid, hipStream_t st) {
 template <typename T>
 int launch_mfma(int d, const DecodeArgs& a, dim3 grid, hipStream_t st) {
   if (d == 64) {
-    k_decode_mfma<T, 64, EMBER_DECODE_KT64, EMBER_DECODE_PF64 != 0><<<grid, kWaves * kWave, 0, st>>>(a);
+    k_decode_mfma<T, 64, EMBER_DECODE_KT64, EMBER_DECODE_PF64 != 0, kWaves64>
+        <<<grid, kWaves64 * kWave, 0, st>>>(a);
   } else {
-    k_decode_mfma<T, 128, EMBER_DECODE_KT128, EMBER_DECODE_PF128 != 0><<<grid, kWaves * kWave, 0, st>>>(a);
+    k_decode_mfma<T, 128, EMBER_DECODE_KT128, EMBER_DECODE_PF128 != 0, kWaves128>
+        <<<grid, kWaves128 * kWave, 0, st>>>(a);
   }
   return EMBER_OK;
 }
@@ -691,7 +702,8 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
   // corresponding alignment; anything else runs the fp32 kernel.
   const bool same = q_dtype == cache_dtype && q_dtype != EMBER_F32 && !(flags & EMBER_DECODE_FP32);
   const bool dok = head_dim == 64 || head_dim == 128;
-  const int64_t out_align_elems = head_dim / 16 * 2 >= 16 ? 8 : 4;
+  const int nw = head_dim == 64 ? kWaves64 : kWaves128;
+  const int64_t out_align_elems = head_dim / (nw * kWave / 16);  // the merge's store width
   const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && q_seq_stride % 8 == 0 &&
                        q_head_stride % 8 == 0 && k_block_stride % 8 == 0 && k_slot_stride % 8 == 0 &&
                        k_head_stride % 8 == 0 && v_block_stride % 8 == 0 && v_slot_stride % 8 == 0 &&

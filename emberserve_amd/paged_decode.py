@@ -33,9 +33,7 @@ SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 VARIANTS = ("sum", "dot")
 MAX_SPLITS = 32
 TILE = 32                 # keys per kernel tile
-WAVES_PER_PROGRAM = 4     # waves of one (sequence, KV head, 16-head chunk, split) workgroup
-BYTES_IN_FLIGHT = 16384   # K+V bytes one wave of one workgroup per CU must keep loading
-MIN_KEYS_PER_SPLIT = 256  # two tiles per wave
+MIN_KEYS_PER_SPLIT = 256
 
 
 def interpreter_enabled() -> bool:
@@ -74,22 +72,23 @@ def default_num_splits(batch: int, num_kv_heads: int, max_context: int, device: 
     """Split-K factor from SHAPES only (paged_triton.py:250-276 contract).
 
     `EMBERSERVE_TRITON_SPLITS=<n>` forces a value (1 disables split-K). Otherwise the grid
-    is sized to the chip: one (sequence, KV head, 16-head chunk) workgroup streams
-    32 * head_dim * 4 bytes of K+V per tile and wave, so head_dim 128 wants one workgroup
-    per compute unit and head_dim 64 two (measured on MI355X: 5.9-6.1 TB/s at one
-    workgroup per CU for D=128, more workgroups only add merge work). Contexts are cut into
-    round(target / programs) pieces, at most MAX_SPLITS and never below MIN_KEYS_PER_SPLIT
-    keys each.
+    is sized to one workgroup per compute unit: a (sequence, KV head, 16-head chunk)
+    workgroup (8 waves at head_dim 64, 4 at 128) keeps one CU's share of HBM bandwidth in
+    flight, and more workgroups only add merge work (measured on MI355X, rotated inputs:
+    128 x 2048 keys at D=64 4.8 TB/s unsplit vs 4.4 at 2 splits; 8 x 8192 keys at D=128
+    5.0 TB/s at 4 splits = 256 workgroups). Contexts are cut into round(CUs / programs)
+    pieces, at most MAX_SPLITS and never below MIN_KEYS_PER_SPLIT keys each. `head_dim` is
+    accepted for callers that size by it; the rule does not need it.
     """
     forced = os.environ.get("EMBERSERVE_TRITON_SPLITS")
     if forced:
         return max(1, int(forced))
+    del head_dim
     chunks = 1
     if num_heads is not None and num_kv_heads > 0:
         chunks = -(-(num_heads // num_kv_heads) // 16)
     programs = max(1, batch * num_kv_heads * chunks)
-    per_cu = max(1, BYTES_IN_FLIGHT // (TILE * head_dim * 4))
-    target = per_cu * num_sms(device)
+    target = num_sms(device)
     want = (target + programs // 2) // programs
     by_context = max(1, max_context // MIN_KEYS_PER_SPLIT)
     return max(1, min(MAX_SPLITS, want, by_context))
