@@ -604,6 +604,144 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
   }
 }
 
+// One token per 64-lane workgroup (16-bit activations, the fast path of the MLA op).
+//
+// The whole token is one wave: NVC latent passes (pack lane + 64 i of the R-wide row, a
+// whole-wave DPP reduction), NQ query passes and one key pass. In a head group of L = 2J
+// lanes, lane r holds pack (r >> 1) + J (r & 1) of the head's Dr-wide slice: the L lanes of
+// a group cover the slice's bytes in one instruction (full 128-byte lines at Dr = 64), and
+// each lane's rotation partner (pack i <-> i + J) is lane r ^ 1, whose value arrives as a
+// quad_perm DPP operand of the multiply. The partner product is formed with the sign folded
+// into the sine (first-half lanes multiply by -s), so
+//   first half:  x1 * c + x2 * (-s) == x1 * c - x2 * s
+//   second half: x2 * c + x1 * s
+// bit for bit the reference's separately rounded expression.
+//
+// Measured on MI355X (Moonlight shape, T = 8192, rotated inputs): 11.7 us against 13.9 us
+// for k_mla. All loads are issued before any arithmetic, and every output is selected
+// rather than branched on, so the compiler cannot sink a load under a branch (a sunk q load
+// serialised position -> table -> q and cost 0.7 us).
+template <typename T, typename WT, int VEC, int J, int NQ, int NVC, bool CACHE>
+__global__ void __launch_bounds__(kWave)
+k_mla_tok(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, int64_t kts, T* __restrict__ qpe,
+          int64_t qts, int64_t qhs, int H, const WT* __restrict__ w, float eps, const float* __restrict__ cos_t,
+          const float* __restrict__ sin_t, int64_t trows, int64_t tstride, const int64_t* __restrict__ pos,
+          T* __restrict__ lat, int64_t lts, const int64_t* __restrict__ slots, T* __restrict__ cache,
+          int64_t num_slots, int64_t css, uint32_t* __restrict__ err) {
+  constexpr int L = 2 * J;          // lanes per head slice
+  constexpr int kHeads = kWave / L;  // heads per query pass
+  const int64_t tok = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int r = lane % L;
+  const int64_t pk = ((r >> 1) + J * (r & 1)) * VEC;  // element offset of this lane's pack
+  const int64_t ci = (r >> 1) * VEC;                  // its cos/sin columns
+  const int ncv = R / VEC;
+
+  const int64_t p = pos[tok];  // scalar load (tok is uniform)
+  int64_t slot = 0;
+  if constexpr (CACHE) slot = slots[tok];
+  Pack<T, VEC> cv[NVC];
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) cv[i] = load_stream<T, VEC>(c + tok * cts + static_cast<int64_t>(min(lane + i * kWave, ncv - 1)) * VEC);
+  Pack<T, VEC> qv[NQ];
+  T* qp[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int head = min(i * kHeads + lane / L, H - 1);
+    qp[i] = qpe + tok * qts + static_cast<int64_t>(head) * qhs + pk;
+    qv[i] = load_stream<T, VEC>(qp[i]);
+  }
+  const Pack<T, VEC> kv = load_stream<T, VEC>(kpe + tok * kts + pk);
+  Pack<WT, VEC> wv[NVC];
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) wv[i] = load_pack<WT, VEC>(w + static_cast<int64_t>(min(lane + i * kWave, ncv - 1)) * VEC);
+  const bool bad = p < 0 || p >= trows;
+  const int64_t pc = bad ? 0 : p;
+  float cc[VEC], sn[VEC];
+  load_vals<float, VEC>(cos_t + pc * tstride + ci, cc);
+  load_vals<float, VEC>(sin_t + pc * tstride + ci, sn);
+  // All loads are issued before any arithmetic: the asm memory clobber keeps the IR passes
+  // from moving a load below this point (the weight load otherwise landed behind the query
+  // stores), sched_barrier keeps the machine scheduler from doing so.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Sine with the first-half sign folded in.
+  const uint32_t sm = (r & 1) ? 0u : 0x80000000u;
+  float sx[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) sx[e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, sn[e]) ^ sm);
+  auto rotate = [&](const Pack<T, VEC>& x) {
+    Pack<T, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float f = to_f32(x.v[e]);
+      const float a = f * cc[e];
+      const float b = dpp_f32<kDppQuadSwap1>(f) * sx[e];
+      o.v[e] = from_f32<T>(a + b);
+    }
+    return o;
+  };
+
+  // Stores are unconditional: a lane past the last head (or latent pack) was clamped onto
+  // the last one, loaded the same bytes and computes the same result, so it rewrites
+  // identical bytes. A divergent store guard made the compiler sink the arithmetic under
+  // it and wait for every load before the first store (13.5 us against 11.7 us).
+  // Query heads: rotated in place; a bad position stores them back unchanged.
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const Pack<T, VEC> o = rotate(qv[i]);
+    store_stream<T, VEC>(qp[i], bad ? qv[i] : o);
+  }
+
+  // Latent row.
+  float v[NVC][VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) {
+    const bool ok = lane + i * kWave < ncv;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float f = ok ? to_f32(cv[i].v[e]) : 0.f;
+      v[i][e] = f;
+      ss += f * f;
+    }
+  }
+  const float tot = group_sum<kWave>(ss);
+  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+  T* lrow = lat == nullptr ? nullptr : lat + tok * lts;
+  T* crow = nullptr;
+  if constexpr (CACHE) {
+    if (slot >= 0 && slot < num_slots) {
+      crow = cache + slot * css;
+    } else if (lane == 0) {
+      atomicOr(err, EMBER_ERR_KV_SLOT);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NVC; ++i) {
+    const int64_t vi = min(lane + i * kWave, ncv - 1);
+    Pack<T, VEC> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o.v[e] = from_f32<T>(round_to<T>(to_f32(cv[i].v[e]) * inv) * to_f32(wv[i].v[e]));
+    // Without the cache the latent tensor is always given; an unconditional store also
+    // keeps the weight load from being sunk under a branch, behind the query stores.
+    if (!CACHE || lrow != nullptr) store_stream<T, VEC>(lrow + vi * VEC, o);
+    if (CACHE && crow != nullptr) store_stream<T, VEC>(crow + vi * VEC, o);
+  }
+
+  // The key head: rotated into the latent row's last Dr columns (zeros for a bad position).
+  // Every L-lane group holds the same head, so all groups store it (identical bytes).
+  Pack<T, VEC> ko = rotate(kv);
+  if (bad) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ko.v[e] = from_f32<T>(0.f);
+  }
+  if (!CACHE || lrow != nullptr) store_stream<T, VEC>(lrow + R + pk, ko);
+  if (CACHE && crow != nullptr) store_stream<T, VEC>(crow + R + pk, ko);
+  if (bad && lane == 0) atomicOr(err, EMBER_ERR_ROPE_POS);
+}
+
 // Any shape, any alignment: one wave per token, scalar accesses.
 template <typename T, typename WT>
 __global__ void __launch_bounds__(256)
@@ -668,6 +806,42 @@ struct MlaArgs {
   int64_t css = 0;
 };
 
+template <typename T, typename WT, int VEC, int J, int NQ, int NVC>
+int launch_mla_tok(const MlaArgs& a) {
+#define EMBER_LAUNCH_MLA_TOK(CACHE_)                                                                             \
+  hipLaunchKernelGGL((k_mla_tok<T, WT, VEC, J, NQ, NVC, CACHE_>), dim3(static_cast<uint32_t>(a.ntok)), dim3(kWave), \
+                     0, a.stream, static_cast<const T*>(a.c), a.cts, static_cast<int>(a.R),                      \
+                     static_cast<const T*>(a.kpe), a.kts, static_cast<T*>(a.qpe), a.qts, a.qhs,                  \
+                     static_cast<int>(a.H), static_cast<const WT*>(a.w), a.eps, a.cos_t, a.sin_t, a.trows,        \
+                     a.tstride, a.pos, static_cast<T*>(a.lat), a.lts, a.slots, static_cast<T*>(a.cache),         \
+                     a.num_slots, a.css, a.err)
+  if (a.cache != nullptr) {
+    EMBER_LAUNCH_MLA_TOK(true);
+  } else {
+    EMBER_LAUNCH_MLA_TOK(false);
+  }
+#undef EMBER_LAUNCH_MLA_TOK
+  return launch_status();
+}
+
+template <typename T, typename WT, int VEC, int J>
+int launch_mla_tok_nq(const MlaArgs& a, int nq, int nvc) {
+  if (nvc == 1) {
+    switch (nq) {
+      case 1: return launch_mla_tok<T, WT, VEC, J, 1, 1>(a);
+      case 2: return launch_mla_tok<T, WT, VEC, J, 2, 1>(a);
+      case 4: return launch_mla_tok<T, WT, VEC, J, 4, 1>(a);
+      default: return EMBER_EINVAL;
+    }
+  }
+  switch (nq) {
+    case 1: return launch_mla_tok<T, WT, VEC, J, 1, 2>(a);
+    case 2: return launch_mla_tok<T, WT, VEC, J, 2, 2>(a);
+    case 4: return launch_mla_tok<T, WT, VEC, J, 4, 2>(a);
+    default: return EMBER_EINVAL;
+  }
+}
+
 template <typename T, typename WT, int VEC, int J, int NVC>
 int launch_mla_vec(const MlaArgs& a) {
   // One token per wave task: measured on MI355X (Moonlight shape, T = 8192) TPW = 1, 2, 4
@@ -714,6 +888,19 @@ int launch_mla_typed(const MlaArgs& a) {
                       aligned16(a.w) && aligned16(a.cos_t) && aligned16(a.sin_t) && a.tstride % 4 == 0 &&
                       a.cts % VEC == 0 && a.kts % VEC == 0 && a.qts % VEC == 0 && a.qhs % VEC == 0 &&
                       a.lts % VEC == 0 && (a.cache == nullptr || (aligned16(a.cache) && a.css % VEC == 0));
+  if constexpr (sizeof(T) == 2) {
+    // one token per 64-lane workgroup: up to 4 query passes, up to 2 latent packs per lane
+    const int64_t nq = pow2_ceil(cdiv(a.H * 2 * j, kWave));
+    const int64_t nvc = cdiv(ncv, kWave);
+    if (vec_ok && a.H >= 1 && a.ntok <= 0x7fffffffLL && nq <= 4 && nvc <= 2 && (j == 2 || j == 4 || j == 8)) {
+      switch (j) {
+        case 2: return launch_mla_tok_nq<T, WT, VEC, 2>(a, static_cast<int>(nq), static_cast<int>(nvc));
+        case 4: return launch_mla_tok_nq<T, WT, VEC, 4>(a, static_cast<int>(nq), static_cast<int>(nvc));
+        case 8: return launch_mla_tok_nq<T, WT, VEC, 8>(a, static_cast<int>(nq), static_cast<int>(nvc));
+        default: break;
+      }
+    }
+  }
   if (vec_ok) {
     const int nvc = pow2_ceil(cdiv(ncv, kWave));
     switch (j) {

@@ -471,6 +471,38 @@ def test_mla_small_shapes(dtype):
         assert_bitexact(got_q_pe, want_q_pe, "q_pe")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads,dr,rank", [
+    (3, 32, 64),      # one-token kernel: 4-lane head groups, one partly filled query pass
+    (5, 64, 256),     # 40 of 64 lanes in the query pass
+    (32, 64, 512),    # four query passes
+    (8, 128, 1024),   # 16-lane head groups, two latent packs per lane
+    (64, 64, 512),    # eight query passes: the task-split kernel
+    (16, 64, 1536),   # three latent packs per lane: the task-split kernel
+])
+def test_mla_kernel_shapes(dtype, heads, dr, rank):
+    """Every shape class of the one-token MLA kernel (head-group widths 4/8/16 lanes, 1-4
+    query passes, 1-2 latent packs) and the shapes routed to the task-split kernel, with a
+    bad position in the batch."""
+    n = 37
+    kv_a, q, w, pos = gen.mla_inputs(n, heads, 16, dr, rank, 300, dtype, seed=81)
+    cos, sin = _tables(dr, 300, 1e4)
+    qv = q.view(n, heads, 16 + dr)
+    want_q_pe, want_lat = ref.mla_latent_rope(kv_a[:, :rank], kv_a[:, rank:], qv[..., 16:], w, 1e-6, cos, sin, pos)
+    pos[11] = 300  # out of range: latent key zeroed, q_pe untouched (the oracle's row 11 is not used)
+    qd, kd = q.to(DEV), kv_a.to(DEV)
+    got_q_pe, lat = ops.mla_latent_rope_hip(kd[:, :rank], kd[:, rank:], qd.view(n, heads, 16 + dr)[..., 16:],
+                                            w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    good = torch.ones(n, dtype=torch.bool)
+    good[11] = False
+    assert_ulp(lat[good, :rank], want_lat[good, :rank], ULP[dtype], "latent c")
+    assert_bitexact(lat[good, rank:], want_lat[good, rank:], "latent k_pe")
+    assert_bitexact(got_q_pe[good], want_q_pe[good], "q_pe")
+    assert_bitexact(got_q_pe[11], qv[11, :, 16:], "bad position: q_pe untouched")
+    assert_bitexact(lat[11, rank:], torch.zeros(dr, dtype=dtype), "bad position: latent key zeroed")
+    assert_bitexact(qd.view(n, heads, 16 + dr)[..., :16], qv[..., :16], "q_nope untouched")
+
+
 # ---------------------------------------------------------------- scalar (unaligned) paths
 
 def test_unaligned_views_take_the_scalar_kernels():
