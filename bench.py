@@ -12,6 +12,8 @@ Also printed in the same JSON line:
                 8 TB/s (algorithmic bytes; inputs rotated past the Infinity Cache;
                 back-to-back launches timed with hipEvents)
   us_per_layer  config 4 summed per T, plus the full per-layer elementwise set
+  graph_replay  the Qwen3-8B per-layer kernels of all 36 layers recorded in one hipGraph
+                (torch.cuda.graph) and replayed, against eager launches (wall us per layer)
   roofline      the dominant kernel of the step (add+RMSNorm, T=8192), timed live with
                 hipEvents around back-to-back launches on its launch stream
   cpu_baseline  the CPU oracle (the reference's PyTorch-eager ops restated) on a bounded
@@ -419,6 +421,70 @@ def _run_chain(ops, t, table, s, cos, sin):
     return ops.fused_add_rmsnorm_hip(s["x"], s["r"], s["w"], 1e-6)
 
 
+# ----------------------------------------------------------------------------- graph replay
+
+def _graph_replay(torch, ops, tables, layers=36, reps=20):
+    """The Qwen3-8B decoder's per-layer elementwise kernels (input add+RMSNorm, qk-norm +
+    rope + paged KV write, post-attention add+RMSNorm, silu_and_mul at I = 12288) for all
+    36 layers, recorded once in a torch.cuda.graph (hipGraph) and replayed, against the same
+    launches issued eagerly from Python. Wall time per step / layers; small T is where the
+    host's per-launch cost (Python + ctypes) dominates the eager path."""
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    cos, sin = tables(128, 40960, 1e6)
+    out = {}
+    for t in (1, 256):
+        g = torch.Generator(device=dev)
+        g.manual_seed(7 + t)
+        x = torch.randn((t, 4096), generator=g, device=dev).to(bf)
+        r = torch.randn((t, 4096), generator=g, device=dev).to(bf)
+        w = (torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)
+        qkv = torch.randn((t, 6144), generator=g, device=dev).to(bf)
+        qw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
+        kw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
+        pos = torch.randint(0, 40960, (t,), generator=g, device=dev)
+        gu = torch.randn((t, 2 * 12288), generator=g, device=dev).to(bf)
+        kc = torch.zeros((1024, 16, 8, 128), device=dev, dtype=bf)
+        vc = torch.zeros_like(kc)
+        slots = torch.randperm(1024 * 16, generator=g, device=dev)[:t]
+
+        def step():
+            for _ in range(layers):
+                ops.fused_add_rmsnorm_hip(x, r, w, 1e-6)
+                ops.rope_kv_cache_hip(qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128),
+                                      qkv[:, 5120:].view(t, 8, 128), cos, sin, pos, slots, kc, vc, qw, kw, 1e-6)
+                ops.fused_add_rmsnorm_hip(x, r, w, 1e-6)
+                ops.silu_and_mul_hip(gu)
+
+        def wall(fn):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / reps
+
+        eager = wall(step)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        replay = wall(graph.replay)
+        out[f"qwen3_8b_T{t}"] = {"layers": layers, "kernels_per_layer": 4,
+                                 "eager_us_per_layer": round(eager * 1e6 / layers, 2),
+                                 "graph_us_per_layer": round(replay * 1e6 / layers, 2)}
+        del graph
+        torch.cuda.empty_cache()
+    return out
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def _cpu_baseline(t, budget_s):
@@ -626,6 +692,11 @@ def main() -> int:
             if all(p is not None for p in parts):
                 us_per_layer[f"qwen2.5_7b_layer_T{tt}"] = round(sum(parts), 2)
 
+    graph_rows = None
+    if not args.quick:
+        _log("graph replay")
+        graph_rows = _graph_replay(torch, ops, tables)
+
     cpu = None
     if not args.quick and not args.no_cpu:
         _log("cpu baseline")
@@ -657,6 +728,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "us_per_layer": us_per_layer,
+        "graph_replay": graph_rows,
         "per_op": per_op,
     }
     print(json.dumps(result))

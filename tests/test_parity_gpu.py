@@ -641,6 +641,70 @@ def test_graph_capture_replays_match_eager():
             assert_bitexact(g, wv, f"replay {seed} {name}")
 
 
+def test_graph_capture_multi_layer_with_kv_write():
+    """Three decoder layers of the Qwen3-shaped elementwise kernels (input add+RMSNorm,
+    qk-norm + rope + paged KV write, post-attention add+RMSNorm, silu_and_mul) recorded in
+    one torch.cuda.graph, as a full-step graph runner records them. Each replay (new inputs,
+    new slots, eager work and syncs in between) equals the eager launches bit for bit,
+    KV caches included."""
+    n, hq, hk, d, hidden, inter, layers = 24, 8, 2, 128, 512, 768, 3
+    blocks, bs = 16, 16
+    dt = torch.bfloat16
+    cos, sin = (t.to(DEV) for t in _tables(d, 4096, 1e6))
+    bufs = {name: torch.empty(shape, dtype=dt, device=DEV) for name, shape in
+            [("x", (n, hidden)), ("r", (n, hidden)), ("qkv", (layers, n, (hq + 2 * hk) * d)),
+             ("gu", (n, 2 * inter))]}
+    pos = torch.empty(n, dtype=torch.int64, device=DEV)
+    slots = torch.empty(n, dtype=torch.int64, device=DEV)
+    kc = torch.zeros(layers, blocks, bs, hk, d, dtype=dt, device=DEV)
+    vc = torch.zeros_like(kc)
+    w = torch.randn(hidden, dtype=dt, device=DEV) * 0.1 + 1
+    qw = torch.randn(d, dtype=dt, device=DEV) * 0.1 + 1
+    kw = torch.randn(d, dtype=dt, device=DEV) * 0.1 + 1
+
+    def step(b, kcache, vcache):
+        outs = []
+        for layer in range(layers):
+            normed, res = ops.fused_add_rmsnorm_hip(b["x"], b["r"], w, 1e-6)
+            qkv = b["qkv"][layer]
+            ops.rope_kv_cache_hip(qkv[:, :hq * d].view(n, hq, d), qkv[:, hq * d:(hq + hk) * d].view(n, hk, d),
+                                  qkv[:, (hq + hk) * d:].view(n, hk, d), cos, sin, pos, slots, kcache[layer],
+                                  vcache[layer], qw, kw, 1e-6)
+            normed2, res2 = ops.fused_add_rmsnorm_hip(normed, res, w, 1e-6)
+            outs += [normed2, res2, ops.silu_and_mul_hip(b["gu"])]
+        return outs
+
+    def fill(seed):
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        for t in bufs.values():
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(dt))
+        pos.copy_(torch.randint(0, 4096, (n,), generator=g, device=DEV))
+        slots.copy_(torch.randperm(blocks * bs, generator=g, device=DEV)[:n])
+
+    fill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(bufs, kc, vc)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step(bufs, kc, vc)
+    for seed in range(1, 4):
+        fill(seed)
+        before = {k: v.clone() for k, v in bufs.items()}
+        kc_e, vc_e = kc.clone(), vc.clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs] + [bufs["qkv"].clone(), kc.clone(), vc.clone()]
+        want = step(before, kc_e, vc_e) + [before["qkv"], kc_e, vc_e]
+        torch.cuda.synchronize()
+        names = [f"layer {i // 3} {('normed', 'residual', 'act')[i % 3]}" for i in range(3 * layers)]
+        for g, wv, name in zip(got, want, names + ["qkv (q/k rotated in place)", "k cache", "v cache"]):
+            assert_bitexact(g, wv, f"replay {seed} {name}")
+
+
 # ---------------------------------------------------------------- paged KV-cache writes
 
 @pytest.mark.parametrize("dtype", DTYPES)
