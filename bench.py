@@ -323,6 +323,7 @@ def _ops(torch, ops, tables):
     # Qwen3-8B's (32q/8kv x128 bf16).
     for b in (1, 8, 32, 128):
         decode("decode", b, 2048, 14, 2, 64, f16, "qwen2.5-0.5b")
+    decode("decode", 1, 8192, 32, 8, 128, bf, "qwen3-8b", cpu=False)
     decode("decode", 8, 8192, 32, 8, 128, bf, "qwen3-8b")
     decode("decode", 64, 4096, 32, 8, 128, bf, "qwen3-8b", cpu=False)
 

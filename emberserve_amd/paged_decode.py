@@ -34,6 +34,7 @@ VARIANTS = ("sum", "dot")
 MAX_SPLITS = 32
 TILE = 32                 # keys per kernel tile
 MIN_KEYS_PER_SPLIT = 256
+LONG_SPLIT_KEYS = 1024    # keys per split at which MAX_SPLITS splits are allowed
 
 
 def interpreter_enabled() -> bool:
@@ -77,7 +78,8 @@ def default_num_splits(batch: int, num_kv_heads: int, max_context: int, device: 
     flight, and more workgroups only add merge work (measured on MI355X, rotated inputs:
     128 x 2048 keys at D=64 4.8 TB/s unsplit vs 4.4 at 2 splits; 8 x 8192 keys at D=128
     5.0 TB/s at 4 splits = 256 workgroups). Contexts are cut into round(CUs / programs)
-    pieces, at most MAX_SPLITS and never below MIN_KEYS_PER_SPLIT keys each. `head_dim` is
+    pieces, never below MIN_KEYS_PER_SPLIT keys each, and at most MAX_SPLITS / 2 unless the
+    context gives every one of MAX_SPLITS splits LONG_SPLIT_KEYS keys. `head_dim` is
     accepted for callers that size by it; the rule does not need it.
     """
     forced = os.environ.get("EMBERSERVE_TRITON_SPLITS")
@@ -91,7 +93,12 @@ def default_num_splits(batch: int, num_kv_heads: int, max_context: int, device: 
     target = num_sms(device)
     want = (target + programs // 2) // programs
     by_context = max(1, max_context // MIN_KEYS_PER_SPLIT)
-    return max(1, min(MAX_SPLITS, want, by_context))
+    # The in-kernel merge grows with the split count: 32 splits pay only once every split
+    # holds >= 1024 keys (measured, B = 1, 32q/8kv x 128: ctx 8192 16 splits 28.8 us vs 32
+    # splits 37.8; ctx 16384 38.1 vs 43.2; ctx 32768 56.9 vs 53.9; 14q/2kv x 64 at 8192:
+    # 16.6 vs 21.5).
+    cap = MAX_SPLITS if max_context >= MAX_SPLITS * LONG_SPLIT_KEYS else MAX_SPLITS // 2
+    return max(1, min(cap, want, by_context))
 
 
 def default_variant() -> str:
