@@ -178,6 +178,9 @@ __host__ inline int pow2_ceil(int64_t v) {
 // Returns the device address of this library's error word on the current device.
 __host__ uint32_t* device_error_word();
 
+// Compute units of the current device (cached per device); 0 if the query fails.
+__host__ int device_cu_count();
+
 __host__ inline int launch_status() {
   return hipGetLastError() == hipSuccess ? EMBER_OK : EMBER_ELAUNCH;
 }

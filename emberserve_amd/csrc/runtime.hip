@@ -30,6 +30,17 @@ __host__ uint32_t* device_error_word() {
   return p;
 }
 
+__host__ int device_cu_count() {
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+  cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 }  // namespace ember
 
 extern "C" {

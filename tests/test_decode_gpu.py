@@ -174,6 +174,22 @@ def test_decode_writes_into_provided_out_buffer_and_strided_q():
     _check(out, q, kc, vc, bt, cl, 0.125, True, "out= / strided q")
 
 
+@pytest.mark.parametrize("batch", [1, 2, 40])
+def test_decode_qwen3_small_and_full_grids(batch):
+    """Qwen3-8B geometry (32q/8kv, D=128, bf16) on both sides of the workgroup-shape rule:
+    grids of at most half as many workgroups as CUs run 8 waves per workgroup, larger
+    grids 4. B = 1 and 2 at the default split (16) are small grids; B = 40 is full at any
+    split. Contexts up to 3000 keys, one ending mid-block."""
+    ctx = [3000] if batch == 1 else _ragged(batch, 3000, 16, seed=batch)
+    q, kc, vc, bt, cl = gen.decode_inputs(ctx, 32, 8, 128, 16, torch.bfloat16, seed=70 + batch)
+    dq, dkc, dvc, dbt, dcl = _to_dev(q, kc, vc, bt, cl)
+    for splits in (None, 1, 4):
+        _say(f"decode qwen3 B={batch} splits={splits}")
+        got = paged_attention_decode(dq, dkc, dvc, dbt, dcl, 128 ** -0.5, num_splits=splits)
+        _check(got, q, kc, vc, bt, cl, 128 ** -0.5, True, f"B={batch} splits={splits}")
+    assert _lib.read_errors() == 0
+
+
 def test_decode_full_size_split_invariance_and_sampled_parity():
     """The bench size (128 sequences x 2048 keys, 14q/2kv D=64 fp16, block 16): the default
     split and one split agree within the split-K rounding; four sampled sequences are
