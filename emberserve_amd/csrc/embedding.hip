@@ -44,14 +44,13 @@ struct Unit<1> {
   using type = uint8_t;
 };
 
-// 16-byte units stream (the gathered rows are read once, the output written once).
+// Table rows are read with ordinary (cached) loads and the output rows written with
+// non-temporal stores. Measured on MI355X ([151936, 4096] bf16, T = 8192, rotated ids):
+// non-temporal table loads 25.1 us, cached loads 23.6 us (the copy of the same bytes
+// takes 23.3 us).
 template <typename V>
 __device__ __forceinline__ V load_unit(const V* p) {
-  if constexpr (sizeof(V) == 16) {
-    return __builtin_bit_cast(V, load_stream<uint32_t, 4>(reinterpret_cast<const uint32_t*>(p)));
-  } else {
-    return *p;
-  }
+  return *p;
 }
 
 template <typename V>
