@@ -260,6 +260,44 @@ def _ops(torch, ops, tables):
         out.append(Op("latent_cache_write", cfg, f"latent[{t},576] bf16 -> paged cache", nbytes, make,
                       lambda a: ops.latent_cache_write_hip(a[0], a[1], a[2]), 2 * t * 576 * 2))
 
+    def mixed(cfg, lens, heads, d):
+        """The mixed-step data movement around attention (paged_flash.py:259-277): pack the
+        decode rows and the left-padded prefill rows, then put both outputs back."""
+        from emberserve_amd.mixed import MixedRows, pack_queries, unpack_outputs
+        plan = MixedRows(lens, dev)
+        t = sum(lens)
+        hkv = 4
+        row = heads * d * 2
+        starts = [sum(lens[:i]) for i in range(len(lens))]
+        dec = [s for s, n in zip(starts, lens) if n == 1]
+        pre = [(s, n) for s, n in zip(starts, lens) if n != 1]
+        dec_t = torch.tensor(dec, device=dev)
+        max_q = max(n for _, n in pre)
+
+        def make(i):
+            qkv = randn((t, (heads + 2 * hkv) * d), bf, 150 + i)
+            return (qkv[:, :heads * d].view(t, heads, d), torch.empty((t, heads, d), dtype=bf, device=dev))
+
+        def ours(a):
+            q_dec, q_pad = pack_queries(a[0], plan)
+            unpack_outputs(a[1], q_dec.view(-1, 1, heads, d), q_pad, plan)
+
+        def torch_sequence(a):  # the reference's ops, as paged_flash.py:259-277 issues them
+            q, out = a
+            q_dec = q.index_select(0, dec_t)
+            qpad = q.new_zeros((len(pre), max_q, heads, d))
+            for j, (s, n) in enumerate(pre):
+                qpad[j, max_q - n:] = q[s:s + n]
+            out.index_copy_(0, dec_t, q_dec)
+            for j, (s, n) in enumerate(pre):
+                out[s:s + n] = qpad[j, max_q - n:]
+
+        nbytes = 2 * (t + plan.num_slots) * row + 8 * plan.num_slots
+        shape = f"{len(dec)} decodes + prompts {[n for _, n in pre]}, q [{t},{heads},{d}] bf16"
+        out.append(Op("mixed_pack_unpack", cfg, shape, nbytes, make, ours, 2 * t * (heads + 2 * hkv) * d * 2))
+        out.append(Op("mixed_torch_sequence", cfg, shape + " (reference torch ops on the GPU)", nbytes, make,
+                      torch_sequence, 2 * t * (heads + 2 * hkv) * d * 2))
+
     def mla_cache(cfg, t):
         cos, sin = tables(64, 8192, 5e4)
         blocks, bs = 2 * t // 16, 16
@@ -323,6 +361,10 @@ def _ops(torch, ops, tables):
     # Qwen3-8B's (32q/8kv x128 bf16).
     for b in (1, 8, 32, 128):
         decode("decode", b, 2048, 14, 2, 64, f16, "qwen2.5-0.5b")
+    # The mixed prefill + decode step's query pack / output unpack at the reference's 7B
+    # mixed-step profile shape (results/tail/profile_mixed_39x300.txt: 39 decodes + one
+    # 300-token prompt, Qwen2.5-7B 28 heads x 128).
+    mixed("mixed", [1] * 39 + [300], 28, 128)
     decode("decode", 1, 8192, 32, 8, 128, bf, "qwen3-8b", cpu=False)
     decode("decode", 8, 8192, 32, 8, 128, bf, "qwen3-8b")
     decode("decode", 64, 4096, 32, 8, 128, bf, "qwen3-8b", cpu=False)

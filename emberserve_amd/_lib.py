@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -21,6 +21,7 @@ ERR_ROPE_POS = 2
 ERR_KV_SLOT = 4
 ERR_DECODE_CTX = 8
 ERR_BLOCK_ID = 16
+ERR_ROW_INDEX = 32
 DECODE_FP32 = 1
 
 _DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -40,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "ember_rope": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p],
     "ember_silu_and_mul": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "ember_embedding": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p],
+    "ember_gather_rows": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
+    "ember_scatter_rows2": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p],
     "ember_qk_norm_rope": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _p, _i32, _f32,
                            _p, _p, _i64, _i64, _p, _i64, _i32, _p],
     "ember_mla_latent_rope": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _f32,

@@ -74,6 +74,8 @@ def _raise_index_errors() -> None:
         raise IndexError("emberserve_amd.rope: position out of range of the cos/sin table")
     if flags & _lib.ERR_KV_SLOT:
         raise IndexError("emberserve_amd.kv_cache_write: slot out of range of the cache")
+    if flags & _lib.ERR_ROW_INDEX:
+        raise IndexError("emberserve_amd.mixed: row index out of range")
 
 
 _EALIGN = 2  # EMBER_EALIGN: a fused entry point refused misaligned operands, nothing ran

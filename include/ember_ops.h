@@ -45,6 +45,10 @@
  *                             (kernels :95-209; fp32 definition attn/paged_torch.py:87-98)
  *   ember_paged_decode_workspace_bytes  the split-K scratch size (_Scratch,
  *                             attn/paged_triton.py:293-310)
+ *   ember_gather_rows         the query pack of a mixed step: index_select + new_zeros +
+ *                             padded copies, attn/paged_flash.py:259-275
+ *   ember_scatter_rows2       the output unpack: index_copy_ + slice copies,
+ *                             attn/paged_flash.py:267,276-277
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
@@ -73,6 +77,7 @@ extern "C" {
 #define EMBER_ERR_KV_SLOT 4u    /* a cache slot outside [0, num_slots) */
 #define EMBER_ERR_DECODE_CTX 8u /* a context length outside [0, max_blocks * block_size] */
 #define EMBER_ERR_BLOCK_ID 16u  /* a block-table entry outside [0, num_blocks) */
+#define EMBER_ERR_ROW_INDEX 32u /* a row index past the end in ember_gather_rows / ember_scatter_rows2 */
 
 /* ABI version, bumped when an entry point is added or its signature changes. */
 int ember_abi_version(void);
@@ -165,6 +170,28 @@ int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora
                           int64_t table_rows, int64_t table_row_stride,
                           const int64_t* positions, int64_t num_tokens,
                           void* latent, int64_t latent_token_stride, int dtype, void* stream);
+
+/* Row gather with padding (the query pack of a mixed prefill + decode step, replacing
+ * q.index_select(0, dec_tokens), q.new_zeros(...) and the per-sequence copies into it at
+ * emberserve/attn/paged_flash.py:259-275): dst[t, :] = src[rows[t], :] for rows[t] in
+ * [0, src_rows); a negative rows[t] is a padding row, written as zeros; rows[t] >= src_rows
+ * writes zeros and sets EMBER_ERR_ROW_INDEX. Rows are row_elems elements of elem_bytes
+ * bytes (1, 2, 4 or 8), strides in elements. Bit-exact. */
+int ember_gather_rows(const void* src, int64_t src_rows, int64_t src_row_stride,
+                      const int64_t* rows, int64_t num_rows,
+                      void* dst, int64_t dst_row_stride,
+                      int64_t row_elems, int64_t elem_bytes, void* stream);
+
+/* Two-source row scatter (the output unpack of the same step, replacing
+ * out.index_copy_(0, dec_tokens, o) and out[start:start + n] = o_pad[i, max_q - n:] at
+ * paged_flash.py:267,276-277): packed row t < src0_rows is src0[t], row t >= src0_rows is
+ * src1[t - src0_rows]; it is copied to dst[rows[t]]. A negative rows[t] is a padding row
+ * and is dropped; rows[t] >= dst_rows is dropped and sets EMBER_ERR_ROW_INDEX. src0 or
+ * src1 may be null when it has no rows. Bit-exact. */
+int ember_scatter_rows2(const void* src0, int64_t src0_rows, int64_t src0_row_stride,
+                        const void* src1, int64_t src1_rows, int64_t src1_row_stride,
+                        const int64_t* rows, void* dst, int64_t dst_rows, int64_t dst_row_stride,
+                        int64_t row_elems, int64_t elem_bytes, void* stream);
 
 /* Paged KV-cache write (PagedKVCache.write, kv/cache.py:54-61, an index_copy_ per tensor):
  *   k_cache[slot_mapping[t], h, :] = k[t, h, :]

@@ -23,6 +23,8 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                columns bit-exact.
   kv_cache_write, latent_cache_write  an explicit per-token loop of slice assignments
                                (slot by slot), bit-exact; untouched slots stay untouched.
+  mixed_pack, mixed_unpack     a per-element Python definition on small inputs (slot by
+                               slot, zero padding); unpack(pack(q)) == q for every mix.
   gather_batch, paged_decode   float64 brute force over the block table, key by key
                                (math.exp, Python sums); one key gives its V row; equal
                                keys give the mean of V; relocating blocks leaves the result
@@ -205,3 +207,44 @@ def paged_decode_prob_mass(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
     probs = torch.softmax(scores, dim=-1)
     return torch.einsum("bhk,bkhd->bhd", probs, vf.abs())
+
+
+def mixed_rows(query_lens):
+    """MixedPlan.build's row bookkeeping (emberserve/attn/paged_flash.py:127-150): packed
+    start of each decode row (query_len == 1) and (start, n) of each prefill row."""
+    dec, pre, start = [], [], 0
+    for n in query_lens:
+        if n == 1:
+            dec.append(start)
+        else:
+            pre.append((start, n))
+        start += n
+    return dec, pre
+
+
+def mixed_pack(q: torch.Tensor, query_lens):
+    """The query side of PagedFlashAttentionBackend._prefill_kvcache (paged_flash.py:
+    259-272): q.index_select(0, dec_tokens) for the decode rows; the prefill rows
+    left-padded into q.new_zeros((P, max_q, H, D)). Returns (q_dec or None, qpad or None)."""
+    dec, pre = mixed_rows(query_lens)
+    q_dec = q.index_select(0, torch.tensor(dec, dtype=torch.long)) if dec else None
+    qpad = None
+    if pre:
+        max_q = max(n for _, n in pre)
+        qpad = q.new_zeros((len(pre), max_q) + tuple(q.shape[1:]))
+        for i, (start, n) in enumerate(pre):
+            qpad[i, max_q - n:] = q[start:start + n]
+    return q_dec, qpad
+
+
+def mixed_unpack(out: torch.Tensor, o_dec, o_pad, query_lens) -> torch.Tensor:
+    """The output side (paged_flash.py:267, 276-277): out.index_copy_(0, dec_tokens, o_dec)
+    and out[start:start + n] = o_pad[i, max_q - n:]. In place on out; returns it."""
+    dec, pre = mixed_rows(query_lens)
+    if dec:
+        out.index_copy_(0, torch.tensor(dec, dtype=torch.long), o_dec.reshape((len(dec),) + tuple(out.shape[1:])))
+    if pre:
+        max_q = o_pad.shape[1]
+        for i, (start, n) in enumerate(pre):
+            out[start:start + n] = o_pad[i, max_q - n:]
+    return out

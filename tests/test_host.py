@@ -253,3 +253,19 @@ def test_paged_decode_default_splits_follow_the_grid_rule(monkeypatch):
     assert pd.default_num_splits(4, 2, 100000, dev, 40, 64) == 16      # 20 heads/kv: 2 chunks
     monkeypatch.setenv("EMBERSERVE_TRITON_SPLITS", "3")
     assert pd.default_num_splits(128, 8, 2048, dev, 32, 128) == 3
+
+
+def test_mixed_rows_plan_and_layout_checks():
+    """MixedRows on the host: slot order (decode rows first, then each prefill row
+    left-padded to max_q), the reference plan's dec_tokens, and refusals before launch."""
+    from emberserve_amd.mixed import MixedRows, pack_queries
+    plan = MixedRows([1, 3, 1, 2], "cpu")
+    assert plan.num_tokens == 7 and plan.num_dec == 2 and plan.num_pre == 2 and plan.max_q == 3
+    assert plan.rows.tolist() == [0, 4, 1, 2, 3, -1, 5, 6]
+    assert plan.dec_tokens.tolist() == [0, 4]
+    assert MixedRows([1, 1], "cpu").rows.tolist() == [0, 1]
+    assert MixedRows([4], "cpu").rows.tolist() == [0, 1, 2, 3]
+    with pytest.raises(ValueError):
+        MixedRows([1, 0], "cpu")
+    with pytest.raises(ValueError):  # host tensors never reach a kernel
+        pack_queries(torch.zeros(7, 2, 4), plan)

@@ -406,3 +406,46 @@ def test_paged_decode_prob_mass_bounds_the_output():
     mass = ref.paged_decode_prob_mass(q, kc, vc, bt, ctx, 0.25)
     assert bool((out.abs() <= mass + 1e-6).all())
     assert bool((mass <= vc.abs().amax() + 1e-6).all())
+
+
+# ---------------------------------------------------------------- mixed-step pack / unpack
+
+_MIXES = [[1, 1, 1], [5], [1, 7, 1, 3, 1], [2, 2], [1, 300, 1, 1], [4, 1, 9]]
+
+
+@pytest.mark.parametrize("lens", _MIXES)
+def test_mixed_pack_matches_the_slot_definition(lens):
+    """Slot by slot on a small input: decode rows in batch order are the packed rows whose
+    sequence has query length 1; prefill sequence p's slot r holds its query
+    r - (max_q - n) (left padding), zeros before that."""
+    T = sum(lens)
+    q = torch.arange(T * 3 * 2, dtype=torch.float32).view(T, 3, 2)
+    q_dec, qpad = ref.mixed_pack(q, lens)
+    starts = [sum(lens[:i]) for i in range(len(lens))]
+    dec = [s for s, n in zip(starts, lens) if n == 1]
+    pre = [(s, n) for s, n in zip(starts, lens) if n != 1]
+    if dec:
+        for i, s in enumerate(dec):
+            assert torch.equal(q_dec[i], q[s])
+    else:
+        assert q_dec is None
+    if pre:
+        max_q = max(n for _, n in pre)
+        assert qpad.shape == (len(pre), max_q, 3, 2)
+        for p, (s, n) in enumerate(pre):
+            for r in range(max_q):
+                j = r - (max_q - n)
+                want = q[s + j] if j >= 0 else torch.zeros(3, 2)
+                assert torch.equal(qpad[p, r], want), (p, r)
+    else:
+        assert qpad is None
+
+
+@pytest.mark.parametrize("lens", _MIXES)
+def test_mixed_unpack_inverts_pack(lens):
+    T = sum(lens)
+    q = _rand(T, 4, 8, dtype=torch.bfloat16, seed=T)
+    q_dec, qpad = ref.mixed_pack(q, lens)
+    out = torch.full_like(q, float("nan"))
+    ref.mixed_unpack(out, q_dec, qpad, lens)
+    assert_bitexact(out, q, "unpack(pack(q))")
