@@ -118,8 +118,13 @@ def _cpu_factories():
                                         lambda: gen.decode_inputs([ctx] * b, hq, hkv, d, 16, dtype, seed=1))
         return lambda: ref.paged_decode(q, kc, vc, bt, cl, d ** -0.5)
 
+    def mla_decode(b, ctx):
+        q, lat, bt, cl = _cpu_inputs(("mla_decode", b, ctx),
+                                     lambda: gen.mla_decode_inputs([ctx] * b, 16, 512, 64, 16, torch.bfloat16, seed=1))
+        return lambda: ref.mla_decode(q[..., :512], q[..., 512:], lat, bt, cl, 192 ** -0.5, 512)
+
     return dict(add_norm=add_norm, rope=rope, silu=silu, embedding=embedding, qk=qk, mla=mla, kv=kv,
-                decode=decode)
+                decode=decode, mla_decode=mla_decode)
 
 
 def _cpu_time_row(fn, budget_s):
@@ -335,6 +340,24 @@ def _ops(torch, ops, tables):
                       nbytes, make, lambda a: paged_attention_decode(a[0], a[1], a[2], a[3], a[4], d ** -0.5),
                       kv_bytes, cpu=("decode", (b, ctx, hq, hkv, d, dtype)) if cpu else None))
 
+    def mla_decode(cfg, b, ctx, label, cpu=True):
+        from emberserve_amd.mla_decode import mla_decode as mla_decode_hip
+        bs, dl, dr, h = 16, 512, 64, 16
+        per = -(-ctx // bs)
+        nblk = b * per + 1
+
+        def make(i):
+            lat = randn((nblk, bs, dl + dr), bf, 240 + i, std=0.5)
+            g.manual_seed(250 + i)  # scrambled block tables
+            bt = torch.randperm(nblk, generator=g, device=dev)[: b * per].to(torch.int32).view(b, per)
+            return (randn((b, h, dl + dr), bf, 260 + i, std=0.5), lat, bt,
+                    torch.full((b,), ctx, dtype=torch.int32, device=dev))
+        lat_bytes = b * ctx * (dl + dr) * 2
+        nbytes = lat_bytes + b * h * (2 * dl + dr) * 2 + 4 * b * (per + 1)  # rows, q + out, tables + lengths
+        out.append(Op("mla_decode", cfg, f"{label}: B={b} ctx={ctx} {h} heads, latent {dl}+{dr} bf16 block {bs}",
+                      nbytes, make, lambda a: mla_decode_hip(a[0], a[1], a[2], a[3], 192 ** -0.5, dl),
+                      lat_bytes, cpu=("mla_decode", (b, ctx)) if cpu else None))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -368,6 +391,13 @@ def _ops(torch, ops, tables):
     decode("decode", 1, 8192, 32, 8, 128, bf, "qwen3-8b", cpu=False)
     decode("decode", 8, 8192, 32, 8, 128, bf, "qwen3-8b")
     decode("decode", 64, 4096, 32, 8, 128, bf, "qwen3-8b", cpu=False)
+    # Absorbed-form MLA decode over the latent cache (attn/mla_triton.py:119-182) at the
+    # Moonlight geometry: the reference's serving profile (results/profile_moonlight_v3.json,
+    # batch 128, 256-token prompts) and longer contexts.
+    mla_decode("mla", 1, 320, "moonlight")
+    mla_decode("mla", 128, 320, "moonlight")
+    mla_decode("mla", 32, 4096, "moonlight", cpu=False)
+    mla_decode("mla", 256, 2048, "moonlight", cpu=False)
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
     # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the

@@ -49,6 +49,10 @@
  *                             padded copies, attn/paged_flash.py:259-275
  *   ember_scatter_rows2       the output unpack: index_copy_ + slice copies,
  *                             attn/paged_flash.py:267,276-277
+ *   ember_mla_decode          mla_decode, emberserve/attn/mla_triton.py:119-182 (kernel
+ *                             :49-116; fp32 definition attn/mla_torch.py:33-53)
+ *   ember_mla_decode_workspace_bytes  its split-K scratch size (the _SCRATCH buffers,
+ *                             attn/mla_triton.py:163-166)
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
@@ -290,6 +294,36 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
                        const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
                        int64_t num_splits, int flags, void* workspace, int64_t workspace_bytes,
                        void* out, int64_t out_seq_stride, int64_t out_head_stride, void* stream);
+
+/* Bytes of workspace ember_mla_decode needs for num_splits > 1 (0 for one split), -1 for
+ * invalid arguments: fp32 partials [splits][seqs][heads][kv_lora_rank + 2] and one uint32
+ * arrival counter per (sequence, head). */
+int64_t ember_mla_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, int64_t kv_lora_rank,
+                                         int64_t num_splits);
+
+/* Absorbed-form multi-head latent attention for one query per sequence (mla_decode):
+ *   out[b, h, :] = softmax_j(scale * (q_c[b, h] . c[b, j] + q_pe[b, h] . k_pe[b, j])) @ c[b, j]
+ * for j < context_lens[b], where cache row j of sequence b is latent_cache[block_tables[b,
+ * j / block_size], j % block_size] = [c (kv_lora_rank) | k_pe (rope_dim)], one row shared by
+ * all heads. q_c [num_seqs, num_heads, kv_lora_rank] and q_pe [num_seqs, num_heads, rope_dim]
+ * of q_dtype (unit last stride; q_pe may point into the same rows as q_c, the reference's
+ * single q_abs tensor); the cache [num_blocks, block_size, kv_lora_rank + rope_dim] of
+ * cache_dtype with the given element strides (unit last stride); out [num_seqs, num_heads,
+ * kv_lora_rank] of q_dtype. block_size must be a multiple of 16 and kv_lora_rank + rope_dim
+ * <= 1024. Split-K, workspace, error bits and the zero-context NaN follow ember_paged_decode.
+ * fp16/bf16 q and cache of one dtype at kv_lora_rank 512, rope_dim 64 (DeepSeek-V2/V3,
+ * Moonlight) with 16-byte aligned operands run on MFMA with the reference kernel's tl.dot
+ * numerics (fp32 scores, probabilities rounded to the cache dtype for P.V); every other case
+ * computes in fp32. */
+int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_stride,
+                     const void* q_pe, int64_t qpe_seq_stride, int64_t qpe_head_stride, int q_dtype,
+                     const void* latent_cache, int64_t num_blocks, int64_t block_size,
+                     int64_t kv_lora_rank, int64_t rope_dim,
+                     int64_t cache_block_stride, int64_t cache_slot_stride, int cache_dtype,
+                     const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                     const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                     int64_t num_splits, void* workspace, int64_t workspace_bytes,
+                     void* out, int64_t out_seq_stride, int64_t out_head_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -96,3 +96,26 @@ def decode_inputs(ctx_lens, hq: int, hkv: int, d: int, block: int, dtype, seed: 
         at += n
     q = torch.randn(len(ctx), hq, d, generator=g).to(dtype)
     return q, k_cache, v_cache, tables, torch.tensor(ctx, dtype=torch.int32)
+
+
+def mla_decode_inputs(ctx_lens, num_heads: int, dl: int, dr: int, block: int, dtype, seed: int = 0,
+                      spare_blocks: int = 5, table_width: int | None = None, amp: float = 0.5):
+    """An MLA decode step in the shape of the reference's kernel test
+    (tests/test_mla_triton_gpu.py:27-37): a latent cache [num_blocks, block, DL + DR] of
+    amp * N(0, 1) rows (stale blocks hold real data), scrambled non-contiguous tables with
+    valid padding ids (0), q_abs = [q_c | q_pe] ~ amp * N(0, 1). Returns (q_abs [B, H, DL +
+    DR], latent_cache, block_tables int32, context_lens int32)."""
+    ctx = [int(c) for c in ctx_lens]
+    g = gen(seed)
+    per = [-(-c // block) for c in ctx]
+    num_blocks = sum(per) + spare_blocks
+    width = max(1, max(per) if per else 1) if table_width is None else table_width
+    latent = (torch.randn(num_blocks, block, dl + dr, generator=g) * amp).to(dtype)
+    perm = torch.randperm(num_blocks, generator=g).tolist()
+    tables = torch.zeros(len(ctx), width, dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(per):
+        tables[i, :n] = torch.tensor(perm[at:at + n], dtype=torch.int32)
+        at += n
+    q_abs = (torch.randn(len(ctx), num_heads, dl + dr, generator=g) * amp).to(dtype)
+    return q_abs, latent, tables, torch.tensor(ctx, dtype=torch.int32)

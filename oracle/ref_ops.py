@@ -30,6 +30,12 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                keys give the mean of V; relocating blocks leaves the result
                                unchanged; GQA maps head h to KV head h // G; the per-sequence
                                causal_softmax_attention formulation (attn/base.py:105-128).
+  mla_decode                   float64 brute force over the block table, key by key; one
+                               key gives its c row; equal rows give the mean of c; block
+                               relocation invariance; q_pe = 0 with k_pe = 0 reduces it to
+                               MQA paged_decode over the c part; the non-absorbed per-head
+                               form with random W_UK / W_UV equals the absorbed one
+                               (mla_torch.py:1-17 derivation).
 No function is left unpinned.
 """
 
@@ -207,6 +213,65 @@ def paged_decode_prob_mass(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     scores = scores.masked_fill(~valid[:, None, :], float("-inf"))
     probs = torch.softmax(scores, dim=-1)
     return torch.einsum("bhk,bkhd->bhd", probs, vf.abs())
+
+
+def gather_latent(latent_cache: torch.Tensor, block_table_row: torch.Tensor, n: int) -> torch.Tensor:
+    """emberserve/kv/cache.py (PagedLatentCache.gather): the first n cache rows of one
+    sequence, [n, DL + DR]."""
+    bs = latent_cache.shape[1]
+    idx = block_table_row[:-(-n // bs)].to(dtype=torch.long)
+    return latent_cache[idx].reshape(-1, latent_cache.shape[2])[:n]
+
+
+def mla_attention_absorbed(q_nope: torch.Tensor, q_pe: torch.Tensor, latent: torch.Tensor,
+                           w_uk: torch.Tensor, w_uv: torch.Tensor, scale: float,
+                           kv_lora_rank: int) -> torch.Tensor:
+    """emberserve/attn/mla_torch.py:33-53: one sequence, q [Q, H, .] the last Q positions of
+    a context of latent rows [T, DL + DR]; causal mask; fp32 math; the result in q_nope's
+    dtype."""
+    q_len, t_len = q_nope.shape[0], latent.shape[0]
+    c = latent[:, :kv_lora_rank].float()
+    k_pe = latent[:, kv_lora_rank:].float()
+    q_c = torch.einsum("qhn,hnl->qhl", q_nope.float(), w_uk.float())
+    scores = (torch.einsum("qhl,tl->hqt", q_c, c) + torch.einsum("qhr,tr->hqt", q_pe.float(), k_pe)) * scale
+    pos = torch.arange(t_len - q_len, t_len)[:, None]
+    mask = torch.arange(t_len)[None, :] > pos
+    scores = scores.masked_fill(mask[None], float("-inf"))
+    p = torch.softmax(scores, dim=-1)
+    out_c = torch.einsum("hqt,tl->qhl", p, c)
+    return torch.einsum("qhl,hvl->qhv", out_c, w_uv.float()).to(q_nope.dtype)
+
+
+def mla_decode(q_c: torch.Tensor, q_pe: torch.Tensor, latent_cache: torch.Tensor,
+               block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+               kv_lora_rank: int) -> torch.Tensor:
+    """The raw P.c output of the MLA decode kernel (attn/mla_triton.py:119-182) as the
+    reference's tests define it (tests/test_mla_triton_gpu.py:40-49): per sequence, gather
+    its rows and run mla_attention_absorbed with identity W_UK / W_UV on fp32 inputs.
+    q_c [B, H, DL], q_pe [B, H, DR]; returns fp32 [B, H, DL]."""
+    h = q_c.shape[1]
+    eye = torch.eye(kv_lora_rank).expand(h, kv_lora_rank, kv_lora_rank)
+    outs = []
+    for b in range(q_c.shape[0]):
+        rows = gather_latent(latent_cache, block_tables[b], int(context_lens[b]))
+        outs.append(mla_attention_absorbed(q_c[b][None].float(), q_pe[b][None].float(), rows.float(),
+                                           eye, eye, scale, kv_lora_rank)[0])
+    return torch.stack(outs)
+
+
+def mla_decode_prob_mass(q_c: torch.Tensor, q_pe: torch.Tensor, latent_cache: torch.Tensor,
+                         block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                         kv_lora_rank: int) -> torch.Tensor:
+    """sum_j p_j |c_j| per output element (fp32 [B, H, DL]) under mla_decode's softmax: the
+    scale of the error that rounding the probabilities to the cache dtype before P.c (the
+    reference kernel's tl.dot, attn/mla_triton.py:109) can add."""
+    outs = []
+    for b in range(q_c.shape[0]):
+        rows = gather_latent(latent_cache, block_tables[b], int(context_lens[b])).float()
+        c, k_pe = rows[:, :kv_lora_rank], rows[:, kv_lora_rank:]
+        scores = (q_c[b].float() @ c.T + q_pe[b].float() @ k_pe.T) * scale
+        outs.append(torch.softmax(scores, dim=-1) @ c.abs())
+    return torch.stack(outs)
 
 
 def mixed_rows(query_lens):

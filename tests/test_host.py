@@ -255,6 +255,50 @@ def test_paged_decode_default_splits_follow_the_grid_rule(monkeypatch):
     assert pd.default_num_splits(128, 8, 2048, dev, 32, 128) == 3
 
 
+# ---- MLA decode (host side) ----------------------------------------------------------------
+def test_mla_decode_cpu_path_matches_oracle_and_asserts_like_the_reference():
+    from emberserve_amd.mla_decode import mla_decode
+    q, lat, bt, cl = gen.mla_decode_inputs([5, 19, 40], 4, 32, 16, 16, torch.float32, seed=0)
+    want = ref.mla_decode(q[..., :32], q[..., 32:], lat, bt, cl, 0.3, 32)
+    torch.testing.assert_close(mla_decode(q, lat, bt, cl, 0.3, 32), want, rtol=0, atol=1e-6)
+    got = mla_decode((q[..., :32], q[..., 32:]), lat, bt, cl, 0.3, 32)  # the pair form
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-6)
+    with pytest.raises(AssertionError):  # DR not a power of two >= 16 (mla_triton.py:155)
+        mla_decode(torch.randn(1, 4, 40), torch.randn(2, 16, 40), bt[:1], cl[:1], 0.3, 32)
+    with pytest.raises(AssertionError, match="block_size"):
+        mla_decode(torch.randn(1, 4, 48), torch.randn(2, 8, 48), bt[:1, :1], torch.ones(1, dtype=torch.int32),
+                   0.3, 32)
+
+
+def test_mla_decode_abi_and_split_rule(monkeypatch):
+    from emberserve_amd import mla_decode as md
+    lib = _lib.load()
+    assert lib.ember_mla_decode_workspace_bytes(2, 16, 512, 1) == 0
+    assert lib.ember_mla_decode_workspace_bytes(2, 16, 512, 3) == 3 * 2 * 16 * 514 * 4 + 128
+    assert lib.ember_mla_decode_workspace_bytes(2, 16, 512, 0) == -1
+
+    def call(block_size=16, dl=512, dr=64, splits=1, heads=16):
+        return lib.ember_mla_decode(None, 0, 0, None, 0, 0, 1, None, 4, block_size, dl, dr, 0, 0, 1, None, 0, 1,
+                                    None, 1, heads, 1.0, splits, None, 0, None, 0, 0, None)
+    for bad in (dict(block_size=8), dict(dl=1024), dict(splits=0), dict(heads=0)):
+        assert call(**bad) == 1, bad
+    assert call() == 1  # null pointers
+    monkeypatch.delenv("EMBERSERVE_TRITON_SPLITS", raising=False)
+    monkeypatch.setattr(md, "num_sms", lambda device: 256)
+    dev = torch.device("cpu")
+    assert md.mla_num_splits(128, dev) == 2                          # 128 workgroups -> 256
+    assert md.mla_num_splits(1, dev) == md.MAX_SPLITS
+    assert md.mla_num_splits(1, dev, max_context=320) == 4           # ~sqrt(context / 16)
+    assert md.mla_num_splits(1, dev, max_context=4096) == 16
+    assert md.mla_num_splits(1, dev, max_context=32768) == 45
+    assert md.mla_num_splits(1, dev, max_context=16) == 1
+    assert md.mla_num_splits(8, dev, num_heads=128, max_context=4096) == 4   # 64 workgroups -> 256
+    assert md.mla_num_splits(128, dev, max_context=320) == 2
+    assert md.mla_num_splits(512, dev) == 1
+    monkeypatch.setenv("EMBERSERVE_TRITON_SPLITS", "5")
+    assert md.mla_num_splits(128, dev) == 5
+
+
 def test_mixed_rows_plan_and_layout_checks():
     """MixedRows on the host: slot order (decode rows first, then each prefill row
     left-padded to max_q), the reference plan's dec_tokens, and refusals before launch."""

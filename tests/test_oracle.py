@@ -408,6 +408,108 @@ def test_paged_decode_prob_mass_bounds_the_output():
     assert bool((mass <= vc.abs().amax() + 1e-6).all())
 
 
+# ---------------------------------------------------------------- MLA decode
+
+def _mla_brute_force(q_abs, lat, bt, ctx, scale, dl):
+    """Key by key in float64 Python arithmetic (math.exp, explicit sums)."""
+    qd, ld = q_abs.double().tolist(), lat.double().tolist()
+    B, H, D = q_abs.shape
+    bs = lat.shape[1]
+    out = np.zeros((B, H, dl))
+    for b in range(B):
+        rows = [ld[int(bt[b, j // bs])][j % bs] for j in range(int(ctx[b]))]
+        for h in range(H):
+            s = [scale * sum(qd[b][h][e] * r[e] for e in range(D)) for r in rows]
+            mx = max(s)
+            w = [math.exp(x - mx) for x in s]
+            tot = sum(w)
+            for e in range(dl):
+                out[b, h, e] = sum(wj * r[e] for wj, r in zip(w, rows)) / tot
+    return out
+
+
+def _mla_ref(q_abs, lat, bt, ctx, scale, dl):
+    return ref.mla_decode(q_abs[..., :dl], q_abs[..., dl:], lat, bt, ctx, scale, dl)
+
+
+def test_mla_decode_matches_brute_force():
+    q, lat, bt, ctx = gen.mla_decode_inputs([5, 19, 33], 3, 8, 4, 16, torch.float32, seed=11)
+    out = _mla_ref(q, lat, bt, ctx, 0.4, 8)
+    np.testing.assert_allclose(out.double().numpy(), _mla_brute_force(q, lat, bt, ctx, 0.4, 8), rtol=0, atol=2e-6)
+
+
+def test_mla_decode_single_key_returns_its_latent_row():
+    q, lat, bt, ctx = gen.mla_decode_inputs([1, 1], 4, 16, 8, 16, torch.float32, seed=12)
+    out = _mla_ref(q, lat, bt, ctx, 0.3, 16)
+    for b in range(2):
+        c = lat[int(bt[b, 0]), 0, :16]
+        assert torch.equal(out[b], c.expand(4, 16))
+
+
+def test_mla_decode_zero_query_averages_the_latents():
+    q, lat, bt, ctx = gen.mla_decode_inputs([45], 2, 16, 8, 16, torch.float32, seed=13)
+    q.zero_()  # every score 0 -> uniform attention over the context
+    out = _mla_ref(q, lat, bt, ctx, 0.3, 16)
+    rows = ref.gather_latent(lat, bt[0], 45)
+    expect = rows[:, :16].double().mean(0)
+    for h in range(2):
+        np.testing.assert_allclose(out[0, h].double().numpy(), expect.numpy(), rtol=0, atol=1e-6)
+
+
+def test_mla_decode_is_invariant_to_block_relocation():
+    q, lat, bt, ctx = gen.mla_decode_inputs([23, 48], 4, 16, 8, 16, torch.float32, seed=14)
+    base = _mla_ref(q, lat, bt, ctx, 0.35, 16)
+    perm = torch.randperm(lat.shape[0], generator=gen.gen(15))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    torch.testing.assert_close(_mla_ref(q, lat[perm], inv[bt.long()].to(torch.int32), ctx, 0.35, 16), base,
+                               rtol=0, atol=0)
+
+
+def test_mla_decode_without_rope_part_is_mqa_paged_decode():
+    """q_pe = 0 and k_pe = 0: MQA over the c part with K = V = c, which is paged_decode with
+    one KV head."""
+    q, lat, bt, ctx = gen.mla_decode_inputs([17, 40], 6, 16, 8, 16, torch.float32, seed=16)
+    q[..., 16:] = 0
+    lat[..., 16:] = 0
+    out = _mla_ref(q, lat, bt, ctx, 0.25, 16)
+    c = lat[..., :16].unsqueeze(2).contiguous()  # [blocks, bs, 1, DL]
+    want = ref.paged_decode(q[..., :16].contiguous(), c, c, bt, ctx, 0.25)
+    torch.testing.assert_close(out, want, rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("q_len", [1, 5])
+def test_mla_absorbed_equals_the_per_head_form(q_len):
+    """The absorbed form against the per-head one it is derived from (mla_torch.py:1-17):
+    k_nope[t, h] = W_UK[h] c[t], v[t, h] = W_UV[h] c[t], scores q_nope . k_nope + q_pe . k_pe,
+    causal over the last q_len positions, out = softmax . v."""
+    g = gen.gen(17)
+    T, H, Dn, Dr, Dl, Dv = 20, 3, 6, 4, 16, 5
+    lat = torch.randn(T, Dl + Dr, generator=g, dtype=torch.float64)
+    q_nope = torch.randn(q_len, H, Dn, generator=g, dtype=torch.float64)
+    q_pe = torch.randn(q_len, H, Dr, generator=g, dtype=torch.float64)
+    w_uk = torch.randn(H, Dn, Dl, generator=g, dtype=torch.float64)
+    w_uv = torch.randn(H, Dv, Dl, generator=g, dtype=torch.float64)
+    got = ref.mla_attention_absorbed(q_nope, q_pe, lat, w_uk, w_uv, 0.3, Dl).double()
+    c, k_pe = lat[:, :Dl], lat[:, Dl:]
+    want = torch.empty(q_len, H, Dv, dtype=torch.float64)
+    for i in range(q_len):
+        n = T - q_len + i + 1  # keys visible to query i
+        for h in range(H):
+            k_nope = c[:n] @ w_uk[h].T  # [n, Dn]
+            v = c[:n] @ w_uv[h].T  # [n, Dv]
+            s = (k_nope @ q_nope[i, h] + k_pe[:n] @ q_pe[i, h]) * 0.3
+            want[i, h] = torch.softmax(s, 0) @ v
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_mla_decode_prob_mass_bounds_the_output():
+    q, lat, bt, ctx = gen.mla_decode_inputs([40, 3], 4, 16, 8, 16, torch.float32, seed=18)
+    out = _mla_ref(q, lat, bt, ctx, 0.25, 16)
+    mass = ref.mla_decode_prob_mass(q[..., :16], q[..., 16:], lat, bt, ctx, 0.25, 16)
+    assert bool((out.abs() <= mass + 1e-6).all())
+
+
 # ---------------------------------------------------------------- mixed-step pack / unpack
 
 _MIXES = [[1, 1, 1], [5], [1, 7, 1, 3, 1], [2, 2], [1, 300, 1, 1], [4, 1, 9]]
