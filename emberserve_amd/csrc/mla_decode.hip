@@ -389,21 +389,21 @@ k_mla_mfma(MlaArgs a) {
     for (int i = 0; i < 4; ++i) cb.o[pr][n][hw * (DL / 2) + 16 * dt + 4 * g + i] = o[dt][i];
   __syncthreads();
 
-  // 16 threads per head; thread p of a head owns d = 8p + 128j + [0, 8), j < DL / 128, so a
-  // head's 16 threads store 256 contiguous bytes per j
-  constexpr int PARTS = NP * 2 * kWave / 16;  // 16 or 32: a head's threads sit in one wave
-  constexpr int NJ = DL / (8 * PARTS);
+  // PARTS threads per head (16, or 32 with four streams); thread p of a head owns
+  // d = 4p + 4 PARTS j + [0, 4), j < NJ, so each j of a head's threads is one contiguous run
+  // of 4 PARTS floats: full lines for the partial stores and loads below, 8-byte output
+  // stores that cover 8 PARTS contiguous bytes.
+  constexpr int PARTS = NP * 2 * kWave / 16;
+  constexpr int NJ = DL / (4 * PARTS);
   const int hh = threadIdx.x / PARTS;
-  const int p8 = (threadIdx.x % PARTS) * 8;
+  const int p4 = (threadIdx.x % PARTS) * 4;
   const bool mine = hh < nhc;
   const int head = head0 + hh;
   float mx = -INFINITY;
   float L = 0.f;
-  float acc[NJ][8];
+  f32x4 acc[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (mine) {
     float mw[NP];
 #pragma unroll
@@ -417,21 +417,21 @@ k_mla_mfma(MlaArgs a) {
       L += wt * cb.l[v][hh];
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] += wt * cb.o[v][hh][p8 + 8 * PARTS * j + e];
+        acc[j] += wt * *reinterpret_cast<const f32x4*>(&cb.o[v][hh][p4 + 4 * PARTS * j]);
     }
   }
-  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + p8;
-  if (a.splits == 1) {
-    if (mine) {
+  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + p4;
+  auto store_out = [&](float l) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        Pack<T, 8> r;
+    for (int j = 0; j < NJ; ++j) {
+      Pack<T, 4> r;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r.v[e] = from_f32<T>(acc[j][e] / L);
-        store_pack<T, 8>(orow + 8 * PARTS * j, r);
-      }
+      for (int e = 0; e < 4; ++e) r.v[e] = from_f32<T>(acc[j][e] / l);
+      store_pack<T, 4>(orow + 4 * PARTS * j, r);
     }
+  };
+  if (a.splits == 1) {
+    if (mine) store_out(L);
     return;
   }
 
@@ -442,7 +442,6 @@ k_mla_mfma(MlaArgs a) {
   // resource (uniform base, exact size) addresses them.
   const int64_t stride = int64_t(a.nseq) * a.nh;
   const int64_t row0 = int64_t(b) * a.nh + head0;  // this chunk's first (sequence, head) row
-  const int voff = (hh * DL + p8) * int(sizeof(float));
   if (mine) {
     if (threadIdx.x % PARTS == 0) {
       store_agent(a.part_m + split * stride + row0 + hh, mx);
@@ -451,10 +450,7 @@ k_mla_mfma(MlaArgs a) {
     const Rsrc rs = partial_rsrc(a.part_o + (split * stride + row0) * DL, nhc * DL);
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
-        store_coherent(rs, voff + (8 * PARTS * j + 4 * h2) * int(sizeof(float)),
-                       f32x4{acc[j][4 * h2], acc[j][4 * h2 + 1], acc[j][4 * h2 + 2], acc[j][4 * h2 + 3]});
+      store_coherent(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __shared__ int is_last;
@@ -468,8 +464,8 @@ k_mla_mfma(MlaArgs a) {
   __syncthreads();
   if (!is_last) return;
 
-  // The merge. A head's 16 threads share its splits for the max and the weights (thread p
-  // takes splits p, p + 16, ...; the weights go to LDS), then each thread sums its own d
+  // The merge. A head's threads share its splits for the max and the weights (thread p
+  // takes splits p, p + PARTS, ...; the weights go to LDS), then each thread sums its own d
   // values over every split, four splits of loads in flight at a time.
   const int pp = threadIdx.x % PARTS;
   const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
@@ -489,53 +485,32 @@ k_mla_mfma(MlaArgs a) {
   for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  const int roff = (hr * DL + p8) * int(sizeof(float));
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int roff = (hr * DL + p4) * int(sizeof(float));
   constexpr int SB = 4;  // splits per batch of loads
   int sp = 0;
   for (; sp + SB <= a.splits; sp += SB) {
-    f32x4 v[SB][NJ][2];
+    f32x4 v[SB][NJ];
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const Rsrc rs = partial_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-          v[u][j][h2] = load_coherent(rs, roff + (8 * PARTS * j + 4 * h2) * int(sizeof(float)));
+      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent(rs, roff + 4 * PARTS * j * int(sizeof(float)));
     }
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const float wt = wts[hh * a.splits + sp + u];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] += wt * v[u][j][e >> 2][e & 3];
+      for (int j = 0; j < NJ; ++j) acc[j] += wt * v[u][j];
     }
   }
   for (; sp < a.splits; ++sp) {
     const Rsrc rs = partial_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
     const float wt = wts[hh * a.splits + sp];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const f32x4 v = load_coherent(rs, roff + (8 * PARTS * j + 4 * h2) * int(sizeof(float)));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[j][4 * h2 + e] += wt * v[e];
-      }
+    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent(rs, roff + 4 * PARTS * j * int(sizeof(float)));
   }
-  if (mine) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      Pack<T, 8> r;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) r.v[e] = from_f32<T>(acc[j][e] / gl);
-      store_pack<T, 8>(orow + 8 * PARTS * j, r);
-    }
-  }
+  if (mine) store_out(gl);
 }
 
 constexpr int kAnyMaxD = 1024;          // DL + DR of the fp32 kernel
