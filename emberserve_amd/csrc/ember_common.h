@@ -156,6 +156,52 @@ struct FastDiv {
 
 // ---------------------------------------------------------------- host helpers
 
+// ---------------------------------------------------------------- split-K partials
+
+// Agent-coherent vector accesses for split-K partials that one workgroup writes and another
+// (possibly on another XCD, whose L2 is separate) reads in the same launch: buffer
+// loads/stores with the sc1 cache policy, the bit that agent-scope atomic accesses carry,
+// so stores are written through and loads are served from memory, not a stale L2 line.
+typedef __amdgpu_buffer_rsrc_t CoherentRsrc;
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer, gfx9 format
+constexpr int kPolicySc1 = 16;
+
+template <int V>
+struct FloatVec;
+template <>
+struct FloatVec<2> {
+  typedef float type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct FloatVec<4> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+
+// A resource over `floats` fp32 values from `base` (out-of-range accesses return zero and
+// are dropped by the hardware).
+__device__ __forceinline__ CoherentRsrc coherent_rsrc(const float* base, int floats) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, floats * int(sizeof(float)), kBufferWord3);
+}
+
+template <int V>
+__device__ __forceinline__ void store_coherent(CoherentRsrc r, int byte_off, typename FloatVec<V>::type v) {
+  if constexpr (V == 4) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kPolicySc1);
+  } else {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, byte_off, 0, kPolicySc1);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ typename FloatVec<V>::type load_coherent(CoherentRsrc r, int byte_off) {
+  using F = typename FloatVec<V>::type;
+  if constexpr (V == 4) return __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kPolicySc1));
+  else return __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kPolicySc1));
+}
+
+// ---------------------------------------------------------------- host helpers
 __host__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 __host__ inline int dtype_size(int dtype) {

@@ -117,22 +117,6 @@ __device__ __forceinline__ void store_agent(float* p, float v) {
 __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16-byte agent-coherent accesses to the split partials: buffer loads/stores with the sc1
-// cache policy, the bit the agent-scope atomic accesses above carry, so a partial written on
-// one XCD is read from memory, not from another XCD's stale L2 line.
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer, gfx9 format
-constexpr int kPolicySc1 = 16;
-__device__ __forceinline__ Rsrc partial_rsrc(const float* base, int floats) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, floats * int(sizeof(float)), kBufferWord3);
-}
-__device__ __forceinline__ void store_coherent(Rsrc r, int byte_off, f32x4 v) {
-  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kPolicySc1);
-}
-__device__ __forceinline__ f32x4 load_coherent(Rsrc r, int byte_off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kPolicySc1));
-}
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
@@ -447,10 +431,10 @@ k_mla_mfma(MlaArgs a) {
       store_agent(a.part_m + split * stride + row0 + hh, mx);
       store_agent(a.part_l + split * stride + row0 + hh, L);
     }
-    const Rsrc rs = partial_rsrc(a.part_o + (split * stride + row0) * DL, nhc * DL);
+    const CoherentRsrc rs = coherent_rsrc(a.part_o + (split * stride + row0) * DL, nhc * DL);
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
-      store_coherent(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
+      store_coherent<4>(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __shared__ int is_last;
@@ -493,9 +477,9 @@ k_mla_mfma(MlaArgs a) {
     f32x4 v[SB][NJ];
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
-      const Rsrc rs = partial_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
+      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
     }
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
@@ -505,10 +489,10 @@ k_mla_mfma(MlaArgs a) {
     }
   }
   for (; sp < a.splits; ++sp) {
-    const Rsrc rs = partial_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
+    const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
     const float wt = wts[hh * a.splits + sp];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
   }
   if (mine) store_out(gl);
 }

@@ -382,17 +382,24 @@ k_decode_mfma(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) cb.o[w][n][16 * dt + 4 * g + i] = o[dt][i];
   __syncthreads();
 
-  constexpr int PARTS = NW * kWave / 16;  // threads per head in the merge
+  // PARTS threads per head; thread p of a head owns d = VEC p + VEC PARTS j + [0, VEC),
+  // j < NJ, so each j of a head's threads is one contiguous run of VEC PARTS floats: whole
+  // lines for the partial stores and loads below.
+  constexpr int PARTS = NW * kWave / 16;
   constexpr int PER = D / PARTS;           // d values per thread
+  constexpr int VEC = PER < 4 ? PER : 4;   // floats per access
+  constexpr int NJ = PER / VEC;
+  static_assert(VEC == 2 || VEC == 4, "merge layout");
+  using FV = typename FloatVec<VEC>::type;
   const int hh = threadIdx.x / PARTS;
-  const int d0 = (threadIdx.x % PARTS) * PER;
+  const int pv = (threadIdx.x % PARTS) * VEC;
   const bool mine = hh < nhc;
   const int head = head0 + hh;
   float mx = -INFINITY;
   float L = 0.f;
-  float acc[PER];
+  FV acc[NJ];
 #pragma unroll
-  for (int e = 0; e < PER; ++e) acc[e] = 0.f;
+  for (int j = 0; j < NJ; ++j) acc[j] = FV{};
   if (mine) {
     float mw[NW];
 #pragma unroll
@@ -405,17 +412,21 @@ k_decode_mfma(DecodeArgs a) {
       const float wt = mw[v] == -INFINITY ? 0.f : exp2_fast(mw[v] - mx);
       L += wt * cb.l[v][hh];
 #pragma unroll
-      for (int e = 0; e < PER; ++e) acc[e] += wt * cb.o[v][hh][d0 + e];
+      for (int j = 0; j < NJ; ++j) acc[j] += wt * *reinterpret_cast<const FV*>(&cb.o[v][hh][pv + VEC * PARTS * j]);
     }
   }
-  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + d0;
-  if (a.splits == 1) {
-    if (mine) {
-      Pack<T, PER> r;
+  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + pv;
+  auto store_out = [&](float l) {
 #pragma unroll
-      for (int e = 0; e < PER; ++e) r.v[e] = from_f32<T>(acc[e] / L);
-      store_pack<T, PER>(orow, r);
+    for (int j = 0; j < NJ; ++j) {
+      Pack<T, VEC> r;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r.v[e] = from_f32<T>(acc[j][e] / l);
+      store_pack<T, VEC>(orow + VEC * PARTS * j, r);
     }
+  };
+  if (a.splits == 1) {
+    if (mine) store_out(L);
     return;
   }
 
@@ -423,49 +434,89 @@ k_decode_mfma(DecodeArgs a) {
   // chunk) to arrive merges all of them (paged_triton.py:188-209 as a kernel epilogue, so
   // no second launch). The arrival counter returns to zero for the next launch.
   // Coherence across the XCDs' separate L2s without writing back whole caches: partials
-  // go out as agent-scope atomic stores (written through to memory), the counter is bumped
-  // only after they have completed (s_waitcnt vmcnt(0)), and the merging workgroup reads
-  // them with agent-scope atomic loads.
+  // go out as agent-coherent (sc1, written-through) stores, the counter is bumped only
+  // after they have completed (s_waitcnt vmcnt(0)), and the merging workgroup reads them
+  // with agent-coherent loads. The chunk's partial rows of one split are contiguous, so one
+  // buffer resource (uniform base, exact size) addresses them.
   const int64_t stride = int64_t(a.nseq) * a.nh;
-  const int64_t row = int64_t(split) * stride + int64_t(b) * a.nh + head;
+  const int64_t row0 = int64_t(b) * a.nh + head0;
   if (mine) {
     if (threadIdx.x % PARTS == 0) {
-      store_agent(a.part_m + row, mx);
-      store_agent(a.part_l + row, L);
+      store_agent(a.part_m + split * stride + row0 + hh, mx);
+      store_agent(a.part_l + split * stride + row0 + hh, L);
     }
+    const CoherentRsrc rs = coherent_rsrc(a.part_o + (split * stride + row0) * D, nhc * D);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) store_agent(a.part_o + row * D + d0 + e, acc[e]);
+    for (int j = 0; j < NJ; ++j)
+      store_coherent<VEC>(rs, (hh * D + pv + VEC * PARTS * j) * int(sizeof(float)), acc[j]);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __shared__ int is_last;
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t* cnt = a.counters + int64_t(b) * a.nh + head0;
+    uint32_t* cnt = a.counters + row0;
     const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == static_cast<uint32_t>(a.splits - 1);
     if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (!is_last || !mine) return;
-  const int64_t hrow = int64_t(b) * a.nh + head;
+  if (!is_last) return;
+
+  // The merge. The global max: a head's threads share its splits (thread p takes splits
+  // p, p + PARTS, ...). Then, per chunk of kWtChunk splits, the weights go to LDS
+  // (split-parallel again) and every thread sums its own d values over the chunk's
+  // splits, four splits of loads in flight at a time.
+  const int pp = threadIdx.x % PARTS;
+  const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
   float gm = -INFINITY;
-  for (int sp = 0; sp < a.splits; ++sp) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + hrow));
+  for (int sp = pp; sp < a.splits; sp += PARTS) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + row0 + hr));
+#pragma unroll
+  for (int k = 1; k < PARTS; k <<= 1) gm = fmaxf(gm, shfl_xor_f(gm, k));
+  constexpr int kWtChunk = 128;
+  static_assert(16 * kWtChunk * int(sizeof(float)) <= kLdsBytes, "weights chunk");
+  float* wts = reinterpret_cast<float*>(lds);  // [16][kWtChunk]; the Combine area is free now
   float gl = 0.f;
-  float gacc[PER];
 #pragma unroll
-  for (int e = 0; e < PER; ++e) gacc[e] = 0.f;
-  for (int sp = 0; sp < a.splits; ++sp) {
-    const int64_t r = sp * stride + hrow;
-    const float ms = load_agent(a.part_m + r);
-    const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
-    gl += wt * load_agent(a.part_l + r);
+  for (int j = 0; j < NJ; ++j) acc[j] = FV{};
+  const int roff = (hr * D + pv) * int(sizeof(float));
+  for (int c0 = 0; c0 < a.splits; c0 += kWtChunk) {
+    const int cn = min(kWtChunk, a.splits - c0);
+    __syncthreads();  // the previous chunk's weights are consumed
+    for (int u = pp; u < cn; u += PARTS) {
+      const int64_t r = (c0 + u) * stride + row0 + hr;
+      const float ms = load_agent(a.part_m + r);
+      const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
+      gl += wt * load_agent(a.part_l + r);
+      wts[hh * kWtChunk + u] = wt;
+    }
+    __syncthreads();
+    constexpr int SB = 4;  // splits per batch of loads
+    int u = 0;
+    for (; u + SB <= cn; u += SB) {
+      FV v[SB][NJ];
 #pragma unroll
-    for (int e = 0; e < PER; ++e) gacc[e] += wt * load_agent(a.part_o + r * D + d0 + e);
+      for (int q = 0; q < SB; ++q) {
+        const CoherentRsrc rs = coherent_rsrc(a.part_o + ((c0 + u + q) * stride + row0) * D, nhc * D);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) v[q][j] = load_coherent<VEC>(rs, roff + VEC * PARTS * j * int(sizeof(float)));
+      }
+#pragma unroll
+      for (int q = 0; q < SB; ++q) {
+        const float wt = wts[hh * kWtChunk + u + q];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] += wt * v[q][j];
+      }
+    }
+    for (; u < cn; ++u) {
+      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((c0 + u) * stride + row0) * D, nhc * D);
+      const float wt = wts[hh * kWtChunk + u];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<VEC>(rs, roff + VEC * PARTS * j * int(sizeof(float)));
+    }
   }
-  Pack<T, PER> res;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) res.v[e] = from_f32<T>(gacc[e] / gl);
-  store_pack<T, PER>(orow, res);
+  for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
+  if (mine) store_out(gl);
 }
 
 // Any geometry: one wave per (sequence, query head, split), fp32 math.
@@ -715,7 +766,7 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
   const int ncu = device_cu_count();
   const bool small_grid = head_dim == 128 && ncu > 0 && progs * num_splits * 2 <= ncu;
   const int nw = head_dim == 64 ? kWaves64 : (small_grid ? kWaves128Small : kWaves128);
-  const int64_t out_align_elems = head_dim / (nw * kWave / 16);  // the merge's store width
+  const int64_t out_align_elems = std::min<int64_t>(4, head_dim / (nw * kWave / 16));  // the merge's store width
   const bool aligned = aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && q_seq_stride % 8 == 0 &&
                        q_head_stride % 8 == 0 && k_block_stride % 8 == 0 && k_slot_stride % 8 == 0 &&
                        k_head_stride % 8 == 0 && v_block_stride % 8 == 0 && v_slot_stride % 8 == 0 &&
