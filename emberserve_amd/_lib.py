@@ -22,6 +22,7 @@ ERR_KV_SLOT = 4
 ERR_DECODE_CTX = 8
 ERR_BLOCK_ID = 16
 ERR_ROW_INDEX = 32
+ERR_SYNC = 64
 DECODE_FP32 = 1
 
 _DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}

@@ -78,6 +78,10 @@ constexpr int kVPad = 8;       // elements of padding per LDS value row (keeps 1
 constexpr float kLazy = 8.f;   // log2 headroom before the running max moves
 constexpr int kMlaPairs = 2;       // tile streams (wave pairs) per workgroup
 constexpr int kMlaPairsSmall = 4;  // ... when the grid fills at most half of the CUs
+#ifndef EMBER_MLA_PAIR_SYNC
+#define EMBER_MLA_PAIR_SYNC 1
+#endif
+constexpr bool kMlaPairSync = EMBER_MLA_PAIR_SYNC != 0;  // pair-local exchange handshake
 constexpr int kMlaDL = 512;
 constexpr int kMlaDR = 64;
 
@@ -108,8 +112,11 @@ struct MlaArgs {
   uint32_t* err;
 };
 
-// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left unconstrained.
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8]):
+// vmcnt(0) alone, lgkmcnt(0) alone.
 constexpr int kWaitVmcnt0 = 0x0F70;
+constexpr int kWaitLgkm0 = 0xC07F;
+constexpr int kSyncSpins = 1 << 15;  // s_sleep(1) polls before a pair wait gives up
 
 __device__ __forceinline__ void store_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -147,7 +154,7 @@ __device__ __forceinline__ void split_range(int ctx, int splits, int split, int&
   t1 = min(t0 + per, nt);
 }
 
-template <typename T, int DL, int DR, int NP>
+template <typename T, int DL, int DR, int NP, bool PSYNC>
 __global__ void __launch_bounds__(NP * 2 * kWave, 2)
 k_mla_mfma(MlaArgs a) {
   using M = MlaMfma<T>;
@@ -255,11 +262,47 @@ k_mla_mfma(MlaArgs a) {
   // receives C[16r + 4g + jj][16dt + n], jj < 4: the A operand's kslots 8g + 4r + jj.
   const T* vtr = vl + (4 * g + (n >> 2)) * VS + 4 * (n & 3);
 
-  // Every wave runs the workgroup's trip count (pair 0's) so that all of them meet the same
-  // barriers; a pair past its own tiles only takes part in them.
-  const int nwg = t1 > t0 ? (t1 - t0 + NP - 1) / NP : 0;
+  // The partner exchange. With PSYNC the two waves of a pair hand their partial scores over
+  // through per-wave LDS counters (a pair runs at its own pace): wave w publishes tile k's
+  // partial once its partner has read tile k-1's (rd of the partner >= k), then bumps its
+  // own wr to k + 1; it reads the partner's partial once the partner's wr reaches k + 1,
+  // then bumps its rd. Each counter has one writer and is written after the data it
+  // covers has completed (s_waitcnt lgkmcnt(0)); LDS serves a CU's waves coherently. Waits
+  // are bounded: a wait that runs out sets EMBER_ERR_SYNC and turns every later wait of
+  // the wave off, so a broken handshake can corrupt a result but never hang the GPU.
+  // Without PSYNC every wave runs the workgroup's trip count (pair 0's) and meets two
+  // workgroup barriers per tile; a pair past its own tiles only takes part in them.
+  __shared__ unsigned sync_wr[NP * 2];
+  __shared__ unsigned sync_rd[NP * 2];
+  bool sync_ok = true;
+  auto pair_wait = [&](const unsigned* cnt, unsigned target) {
+    if (!sync_ok) return;
+    int spins = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSyncSpins) {
+        sync_ok = false;
+        if (lane == 0) atomicOr(a.err, EMBER_ERR_SYNC);
+        break;
+      }
+    }
+    asm volatile("" ::: "memory");
+  };
+  auto pair_post = [&](unsigned* cnt, unsigned v) {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the data this count covers has landed
+    asm volatile("" ::: "memory");
+    __hip_atomic_store(cnt, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  if constexpr (PSYNC) {
+    if (threadIdx.x < NP * 2) {
+      sync_wr[threadIdx.x] = 0;
+      sync_rd[threadIdx.x] = 0;
+    }
+    __syncthreads();
+  }
+  const int nwg = PSYNC ? nloc : (t1 > t0 ? (t1 - t0 + NP - 1) / NP : 0);
   for (int k = 0; k < nwg; ++k) {
-    const bool active = k < nloc;  // uniform over the pair
+    const bool active = PSYNC || k < nloc;  // uniform over the pair
     const int k0 = (t0 + pr + NP * k) * kTile;
     const bool partial = k0 + kTile > kend;
     const bool more = k + 1 < nloc;
@@ -290,17 +333,21 @@ k_mla_mfma(MlaArgs a) {
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int j = 0; j < NV; ++j) store_pack<T, 8>(vl + (16 * s + n) * VS + 32 * j + 8 * g, kr[s][j]);
+      if constexpr (PSYNC) pair_wait(&sync_rd[w ^ 1], k);
       xs[(w * 2 + 0) * kWave + lane] = sc[0];
       xs[(w * 2 + 1) * kWave + lane] = sc[1];
+      if constexpr (PSYNC) pair_post(&sync_wr[w], k + 1);
       asm volatile("" ::: "memory");
       // the registers take the pair's next tile while this one's exchange, softmax and P.V
       // run
       if (more) load_tile(k + 1);
     }
-    __syncthreads();
+    if constexpr (PSYNC) pair_wait(&sync_wr[w ^ 1], k + 1);
+    else __syncthreads();
     if (active) {
       sc[0] += xs[((w ^ 1) * 2 + 0) * kWave + lane];
       sc[1] += xs[((w ^ 1) * 2 + 1) * kWave + lane];
+      if constexpr (PSYNC) pair_post(&sync_rd[w], k + 1);
 
       float x[8];
 #pragma unroll
@@ -355,7 +402,7 @@ k_mla_mfma(MlaArgs a) {
       }
     }
     // the partner has read this tile's partial scores before the next tile's land
-    __syncthreads();
+    if constexpr (!PSYNC) __syncthreads();
   }
 
   // merge the tile streams (the two waves of a pair hold the same m and l)
@@ -741,14 +788,14 @@ int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_str
     const bool small = ncu > 0 && progs * num_splits * 2 <= ncu;
     if (q_dtype == EMBER_F16) {
       if (small)
-        k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairsSmall><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
+        k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairsSmall, kMlaPairSync><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
       else
-        k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairs><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
+        k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairs, kMlaPairSync><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
     } else {
       if (small)
-        k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairsSmall><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
+        k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairsSmall, kMlaPairSync><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
       else
-        k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairs><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
+        k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairs, kMlaPairSync><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
     }
   } else {
     dim3 grid(static_cast<uint32_t>(num_seqs * num_heads), static_cast<uint32_t>(num_splits));

@@ -82,6 +82,7 @@ extern "C" {
 #define EMBER_ERR_DECODE_CTX 8u /* a context length outside [0, max_blocks * block_size] */
 #define EMBER_ERR_BLOCK_ID 16u  /* a block-table entry outside [0, num_blocks) */
 #define EMBER_ERR_ROW_INDEX 32u /* a row index past the end in ember_gather_rows / ember_scatter_rows2 */
+#define EMBER_ERR_SYNC 64u      /* an in-kernel wave handshake timed out (a library fault, never input) */
 
 /* ABI version, bumped when an entry point is added or its signature changes. */
 int ember_abi_version(void);
