@@ -157,4 +157,6 @@ def mla_decode(q_abs: Tensor | tuple[Tensor, Tensor], latent_cache: Tensor, bloc
             raise IndexError("emberserve_amd.mla_decode: context length outside the block table")
         if flags & _lib.ERR_BLOCK_ID:
             raise IndexError("emberserve_amd.mla_decode: block id outside the cache")
+        if flags & _lib.ERR_SYNC:
+            raise RuntimeError("emberserve_amd.mla_decode: an in-kernel wave handshake timed out")
     return out
