@@ -114,6 +114,23 @@ def test_long_contexts_cross_block_id_windows():
     assert _lib.read_errors() == 0
 
 
+def test_full_size_sampled_parity_at_every_split_count():
+    """The bench's largest row (256 sequences x 2048 keys, bf16, block 16) at one split,
+    the default and 8: five sampled sequences of each match the oracle on their own, and
+    no error bit is set."""
+    ctx = [2048] * 256
+    q, lat, bt, cl = gen.mla_decode_inputs(ctx, H, DL, DR, 16, torch.bfloat16, seed=13, spare_blocks=1)
+    dq, dlat, dbt, dcl = (t.to(DEV) for t in (q, lat, bt, cl))
+    for splits in (1, None, 8):
+        _say(f"mla decode full size splits {splits}")
+        got = mla_decode(dq, dlat, dbt, dcl, SCALE, DL, num_splits=splits).cpu()
+        for b in (0, 77, 128, 201, 255):
+            sl = slice(b, b + 1)
+            _check(got[sl], q[sl, :, :DL], q[sl, :, DL:], lat, bt[sl], cl[sl], SCALE, DL, True,
+                   f"splits {splits} sequence {b}")
+    assert _lib.read_errors() == 0
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3])
 def test_interpreter_geometry_fp32(splits):
     """tests/test_mla_triton.py's geometry (H 4, DL 32, DR 16, fp32), its contexts and split
