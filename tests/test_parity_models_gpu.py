@@ -1,0 +1,115 @@
+"""Parity at the shapes of other models the reference's families cover, beyond the
+configurations the main parity file mirrors: the hidden sizes, MLP widths and head layouts
+of the Qwen2.5 / Qwen3 range (0.5B to 72B) and DeepSeek-V2/V3. Each shape takes the kernel
+configuration its size selects (row-team widths, packs per lane, query-head passes), so
+this sweeps those paths against the oracle with the tolerances of tests/test_parity_gpu.py
+(bit-exact residual, rope and embedding; <= 2 ulp for the normalised and silu outputs)."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+from emberserve_amd import _lib, ops  # noqa: E402
+from oracle import inputs as gen  # noqa: E402
+from oracle import ref_ops as ref  # noqa: E402
+from tests.helpers import assert_bitexact, assert_ulp  # noqa: E402
+
+DEV = "cuda"
+BF = torch.bfloat16
+HIDDEN = [1536, 2048, 2560, 5120, 8192, 16384]           # 1.5B, 3B, Qwen3-4B, 32B, 72B, wide
+INTER = [8960, 9728, 13824, 25600, 29568]                 # 1.5B, Qwen3-4B, 14B, Qwen3-32B, 72B
+HEADS = [(12, 2, 128), (16, 8, 128), (40, 8, 128), (64, 8, 128), (128, 8, 128), (16, 2, 64)]
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(autouse=True)
+def _clear_errors():
+    _lib.read_errors(clear=True)
+    yield
+    assert _lib.read_errors() == 0
+
+
+@pytest.mark.parametrize("hidden", HIDDEN)
+@pytest.mark.parametrize("rows", [3, 257])
+def test_add_rmsnorm_model_hidden_sizes(hidden, rows):
+    _say(f"add+rmsnorm hidden={hidden} rows={rows}")
+    x, r, w = gen.add_rmsnorm_inputs(rows, hidden, BF, seed=hidden + rows)
+    got, got_res = ops.fused_add_rmsnorm_hip(x.to(DEV), r.to(DEV), w.to(DEV), 1e-6)
+    want, want_res = ref.fused_add_rmsnorm(x, r, w, 1e-6)
+    assert_bitexact(got_res, want_res, "residual")
+    assert_ulp(got, want, 2, "normed")
+    assert_ulp(ops.rmsnorm_hip(x.to(DEV), w.to(DEV), 1e-6), ref.rmsnorm(x, w, 1e-6), 2, "rmsnorm")
+
+
+@pytest.mark.parametrize("inter", INTER)
+def test_silu_and_mul_model_widths(inter):
+    _say(f"silu_and_mul inter={inter}")
+    x = gen.silu_inputs(65, inter, BF, seed=inter)
+    assert_ulp(ops.silu_and_mul_hip(x.to(DEV)), ref.silu_and_mul(x), 2, "silu_and_mul")
+
+
+@pytest.mark.parametrize("heads", HEADS)
+def test_rope_and_qk_norm_rope_model_heads(heads):
+    """q/k as views of the fused qkv projection output at each head layout; rope bit-exact,
+    qk-norm + rope within the norm's 2 ulp carried through the rotation (+1 ulp)."""
+    hq, hk, d = heads
+    n = 33
+    _say(f"rope / qk-norm heads={heads}")
+    qkv, qw, kw, pos = gen.qkv_inputs(n, hq, hk, d, 32768, BF, seed=hq * 7 + hk)
+    cos, sin = ref.rope_tables(d, 32768, 1e6)
+    q = qkv[:, :hq * d].view(n, hq, d)
+    k = qkv[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    want_q, want_k = ref.rope(q, k, cos, sin, pos)
+    qkv_d = qkv.to(DEV)
+    qd = qkv_d[:, :hq * d].view(n, hq, d)
+    kd = qkv_d[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    ops.rope_hip(qd, kd, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    assert_bitexact(qd, want_q, "rope q")
+    assert_bitexact(kd, want_k, "rope k")
+    assert_bitexact(qkv_d[:, (hq + hk) * d:], qkv[:, (hq + hk) * d:], "v untouched")
+    want_q, want_k = ref.qk_norm_rope(q, k, qw, kw, 1e-6, cos, sin, pos)
+    qkv_d = qkv.to(DEV)
+    qd = qkv_d[:, :hq * d].view(n, hq, d)
+    kd = qkv_d[:, hq * d:(hq + hk) * d].view(n, hk, d)
+    ops.qk_norm_rope_hip(qd, kd, qw.to(DEV), kw.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    assert_ulp(qd, want_q, 3, "qk-norm q")
+    assert_ulp(kd, want_k, 3, "qk-norm k")
+
+
+@pytest.mark.parametrize("hidden", [1536, 5120, 8192])
+def test_embedding_model_tables(hidden):
+    _say(f"embedding hidden={hidden}")
+    ids, w = gen.embedding_inputs(129, 32000, hidden, BF, seed=hidden)
+    assert_bitexact(ops.embedding_hip(ids.to(DEV), w.to(DEV)), ref.embedding(ids, w), "embedding")
+
+
+@pytest.mark.parametrize("heads", [16, 128])
+def test_mla_latent_rope_deepseek_heads(heads):
+    """DeepSeek-V2-Lite / Moonlight (16 heads) and V3 (128 heads): kv_lora_rank 512, rope 64,
+    nope 128."""
+    n = 17
+    _say(f"mla latent heads={heads}")
+    kv_a, q, w, pos = gen.mla_inputs(n, heads, 128, 64, 512, 4096, BF, seed=heads)
+    cos, sin = ref.rope_tables(64, 4096, 5e4)
+    c, k_pe = kv_a[:, :512], kv_a[:, 512:]
+    q_pe = q[..., 128:]
+    want_q, want_latent = ref.mla_latent_rope(c, k_pe, q_pe, w, 1e-6, cos, sin, pos)
+    qd = q.to(DEV)
+    kv_d = kv_a.to(DEV)
+    got_q, got_latent = ops.mla_latent_rope_hip(kv_d[:, :512], kv_d[:, 512:], qd[..., 128:],
+                                                w.to(DEV), 1e-6, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    assert_bitexact(got_q, want_q, "q_pe")
+    assert_bitexact(qd[..., :128], q[..., :128], "q_nope untouched")
+    assert_bitexact(got_latent[:, 512:], want_latent[:, 512:], "k_pe")
+    assert_ulp(got_latent[:, :512], want_latent[:, :512], 2, "latent c")
