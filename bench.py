@@ -555,7 +555,82 @@ def _graph_replay(torch, ops, tables, layers=36, reps=20):
                                  "graph_us_per_layer": round(replay * 1e6 / layers, 2)}
         del graph
         torch.cuda.empty_cache()
+    out.update(_graph_decode_step(torch, ops, tables, layers=layers, reps=reps))
     return out
+
+
+def _graph_decode_step(torch, ops, tables, layers=36, reps=10, batch=64, ctx=2048):
+    """A Qwen3-8B decode step without its GEMMs: per layer add+RMSNorm, qk-norm + rope +
+    paged KV write, paged decode attention over the layer's own cache (batch sequences of
+    ctx keys, block 16, scrambled tables), add+RMSNorm and silu_and_mul, for all 36 layers,
+    eagerly and as one replayed hipGraph. Each layer has its own 268 MB cache, so the 256 MB
+    Infinity Cache cannot serve the next layer's keys."""
+    from emberserve_amd.paged_decode import paged_attention_decode
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    t = batch
+    cos, sin = tables(128, 40960, 1e6)
+    g = torch.Generator(device=dev)
+    g.manual_seed(91)
+    x = torch.randn((t, 4096), generator=g, device=dev).to(bf)
+    r = torch.randn((t, 4096), generator=g, device=dev).to(bf)
+    w = (torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)
+    qkv = torch.randn((t, 6144), generator=g, device=dev).to(bf)
+    qw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
+    kw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
+    gu = torch.randn((t, 2 * 12288), generator=g, device=dev).to(bf)
+    per = ctx // 16
+    nblk = t * per + 1
+    caches = []
+    for _ in range(layers):
+        kc = torch.randn((nblk, 16, 8, 128), generator=g, device=dev).to(bf)
+        caches.append((kc, torch.randn_like(kc)))
+    bt = torch.randperm(nblk, generator=g, device=dev)[:t * per].to(torch.int32).view(t, per)
+    cl = torch.full((t,), ctx, dtype=torch.int32, device=dev)
+    pos = torch.full((t,), ctx - 1, dtype=torch.int64, device=dev)
+    slots = (bt[:, (ctx - 1) // 16].to(torch.int64) * 16 + (ctx - 1) % 16).contiguous()
+    attn = torch.empty((t, 32, 128), dtype=bf, device=dev)
+    q, k, v = qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128)
+
+    def step():
+        for kc, vc in caches:
+            ops.fused_add_rmsnorm_hip(x, r, w, 1e-6)
+            ops.rope_kv_cache_hip(q, k, v, cos, sin, pos, slots, kc, vc, qw, kw, 1e-6)
+            paged_attention_decode(q, kc, vc, bt, cl, 128 ** -0.5, out=attn)
+            ops.fused_add_rmsnorm_hip(x, r, w, 1e-6)
+            ops.silu_and_mul_hip(gu)
+
+    def wall(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    eager = wall(step)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    replay = wall(graph.replay)
+    kv_bytes = t * ctx * 8 * 128 * 2 * 2
+    res = {f"qwen3_8b_decode_B{t}_ctx{ctx}": {
+        "layers": layers, "kernels_per_layer": 5,
+        "eager_us_per_layer": round(eager * 1e6 / layers, 2),
+        "graph_us_per_layer": round(replay * 1e6 / layers, 2),
+        "kv_bytes_per_layer": kv_bytes,
+        "graph_kv_GB_per_s": round(kv_bytes / (replay / layers) / 1e9, 1)}}
+    del graph, caches
+    torch.cuda.empty_cache()
+    return res
 
 
 # ----------------------------------------------------------------------------- CPU baseline
