@@ -82,6 +82,10 @@ constexpr int kMlaPairsSmall = 4;  // ... when the grid fills at most half of th
 #define EMBER_MLA_PAIR_SYNC 1
 #endif
 constexpr bool kMlaPairSync = EMBER_MLA_PAIR_SYNC != 0;  // pair-local exchange handshake
+#ifndef EMBER_MLA_STAGED
+#define EMBER_MLA_STAGED 1
+#endif
+constexpr bool kMlaStaged = EMBER_MLA_STAGED != 0;  // small grids: rows staged through LDS
 constexpr int kMlaDL = 512;
 constexpr int kMlaDR = 64;
 
@@ -116,6 +120,7 @@ struct MlaArgs {
 // vmcnt(0) alone, lgkmcnt(0) alone.
 constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kWaitLgkm0 = 0xC07F;
+constexpr int kWaitVmcnt18 = 0x4F72;  // vmcnt(18): 18 = 0b01'0010 -> [15:14] = 1, [3:0] = 2
 constexpr int kSyncSpins = 1 << 15;  // s_sleep(1) polls before a pair wait gives up
 
 __device__ __forceinline__ void store_agent(float* p, float v) {
@@ -126,6 +131,19 @@ __device__ __forceinline__ float load_agent(const float* p) {
 }
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// One 16-byte-per-lane load from global memory straight to LDS: lane i's 16 bytes land at
+// lds_base + 16 i. Only the device pass sees the builtin (the host pass drops the kernel's
+// launch stub when it appears in a kernel body it does not generate code for).
+__device__ __forceinline__ void load_to_lds16(const void* gptr, void* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)(
+                                             reinterpret_cast<uintptr_t>(lds_base)), 16, 0, 0);
+#else
+  (void)gptr;
+  (void)lds_base;
+#endif
+}
 
 __device__ __forceinline__ int seq_context(const MlaArgs& a, int b) {
   int c = a.ctx[b];
@@ -152,6 +170,165 @@ __device__ __forceinline__ void split_range(int ctx, int splits, int split, int&
   const int per = (nt + splits - 1) / splits;
   t0 = split * per;
   t1 = min(t0 + per, nt);
+}
+
+// The end of an MFMA kernel's workgroup: the tile streams merge through LDS, then either
+// the output rows are written (one split) or the split's partial is published and the last
+// split to arrive merges all of them. m, lsum and o are the wave's online-softmax state;
+// wave w of pair w / 2 holds d in [(w % 2) DL / 2, (w % 2 + 1) DL / 2).
+template <typename T, int DL, int NP>
+__device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds, float m, float lsum,
+                                           const f32x4 (&o)[DL / 32], int b, int split, int head0,
+                                           int nhc) {
+  constexpr int NDT = DL / 32;
+  struct Combine {
+    float m[NP][16];
+    float l[NP][16];
+    float o[NP][16][DL + 4];
+  };
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pr = w >> 1;
+  const int hw = w & 1;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  // merge the tile streams (the two waves of a pair hold the same m and l)
+  lsum += shfl_xor_f(lsum, 16);
+  lsum += shfl_xor_f(lsum, 32);
+  __syncthreads();
+  Combine& cb = *reinterpret_cast<Combine*>(lds);
+  if (g == 0 && hw == 0) {
+    cb.m[pr][n] = m;
+    cb.l[pr][n] = lsum;
+  }
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cb.o[pr][n][hw * (DL / 2) + 16 * dt + 4 * g + i] = o[dt][i];
+  __syncthreads();
+
+  // PARTS threads per head (16, or 32 with four streams); thread p of a head owns
+  // d = 4p + 4 PARTS j + [0, 4), j < NJ, so each j of a head's threads is one contiguous run
+  // of 4 PARTS floats: full lines for the partial stores and loads below, 8-byte output
+  // stores that cover 8 PARTS contiguous bytes.
+  constexpr int PARTS = NP * 2 * kWave / 16;
+  constexpr int NJ = DL / (4 * PARTS);
+  const int hh = threadIdx.x / PARTS;
+  const int p4 = (threadIdx.x % PARTS) * 4;
+  const bool mine = hh < nhc;
+  const int head = head0 + hh;
+  float mx = -INFINITY;
+  float L = 0.f;
+  f32x4 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (mine) {
+    float mw[NP];
+#pragma unroll
+    for (int v = 0; v < NP; ++v) {
+      mw[v] = cb.m[v][hh];
+      mx = fmaxf(mx, mw[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < NP; ++v) {
+      const float wt = mw[v] == -INFINITY ? 0.f : exp2_fast(mw[v] - mx);
+      L += wt * cb.l[v][hh];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[j] += wt * *reinterpret_cast<const f32x4*>(&cb.o[v][hh][p4 + 4 * PARTS * j]);
+    }
+  }
+  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + p4;
+  auto store_out = [&](float l) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      Pack<T, 4> r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r.v[e] = from_f32<T>(acc[j][e] / l);
+      store_pack<T, 4>(orow + 4 * PARTS * j, r);
+    }
+  };
+  if (a.splits == 1) {
+    if (mine) store_out(L);
+    return;
+  }
+
+  // Split-K: publish this split's partial with agent-coherent (sc1, written through) 16-byte
+  // stores, count the arrival once they have completed, and let the last split to arrive
+  // merge all of them with agent-coherent loads; it returns the counter to zero for the next
+  // launch. The workgroup's 16 partial rows of one split are contiguous, so one buffer
+  // resource (uniform base, exact size) addresses them.
+  const int64_t stride = int64_t(a.nseq) * a.nh;
+  const int64_t row0 = int64_t(b) * a.nh + head0;  // this chunk's first (sequence, head) row
+  if (mine) {
+    if (threadIdx.x % PARTS == 0) {
+      store_agent(a.part_m + split * stride + row0 + hh, mx);
+      store_agent(a.part_l + split * stride + row0 + hh, L);
+    }
+    const CoherentRsrc rs = coherent_rsrc(a.part_o + (split * stride + row0) * DL, nhc * DL);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      store_coherent<4>(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __shared__ int is_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = a.counters + row0;
+    const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == static_cast<uint32_t>(a.splits - 1);
+    if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last) return;
+
+  // The merge. A head's threads share its splits for the max and the weights (thread p
+  // takes splits p, p + PARTS, ...; the weights go to LDS), then each thread sums its own d
+  // values over every split, four splits of loads in flight at a time.
+  const int pp = threadIdx.x % PARTS;
+  const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
+  float* wts = reinterpret_cast<float*>(lds);  // [16][splits]; the Combine area is free now
+  float gm = -INFINITY;
+  for (int sp = pp; sp < a.splits; sp += PARTS) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + row0 + hr));
+#pragma unroll
+  for (int k = 1; k < PARTS; k <<= 1) gm = fmaxf(gm, shfl_xor_f(gm, k));
+  float gl = 0.f;
+  for (int sp = pp; sp < a.splits; sp += PARTS) {
+    const float ms = load_agent(a.part_m + sp * stride + row0 + hr);
+    const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
+    gl += wt * load_agent(a.part_l + sp * stride + row0 + hr);
+    wts[hh * a.splits + sp] = wt;
+  }
+#pragma unroll
+  for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int roff = (hr * DL + p4) * int(sizeof(float));
+  constexpr int SB = 4;  // splits per batch of loads
+  int sp = 0;
+  for (; sp + SB <= a.splits; sp += SB) {
+    f32x4 v[SB][NJ];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const float wt = wts[hh * a.splits + sp + u];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] += wt * v[u][j];
+    }
+  }
+  for (; sp < a.splits; ++sp) {
+    const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
+    const float wt = wts[hh * a.splits + sp];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+  }
+  if (mine) store_out(gl);
 }
 
 template <typename T, int DL, int DR, int NP, bool PSYNC>
@@ -405,143 +582,258 @@ k_mla_mfma(MlaArgs a) {
     if constexpr (!PSYNC) __syncthreads();
   }
 
-  // merge the tile streams (the two waves of a pair hold the same m and l)
-  lsum += shfl_xor_f(lsum, 16);
-  lsum += shfl_xor_f(lsum, 32);
-  __syncthreads();
-  Combine& cb = *reinterpret_cast<Combine*>(lds);
-  if (g == 0 && hw == 0) {
-    cb.m[pr][n] = m;
-    cb.l[pr][n] = lsum;
-  }
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cb.o[pr][n][hw * (DL / 2) + 16 * dt + 4 * g + i] = o[dt][i];
-  __syncthreads();
+  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc);
+}
 
-  // PARTS threads per head (16, or 32 with four streams); thread p of a head owns
-  // d = 4p + 4 PARTS j + [0, 4), j < NJ, so each j of a head's threads is one contiguous run
-  // of 4 PARTS floats: full lines for the partial stores and loads below, 8-byte output
-  // stores that cover 8 PARTS contiguous bytes.
-  constexpr int PARTS = NP * 2 * kWave / 16;
-  constexpr int NJ = DL / (4 * PARTS);
-  const int hh = threadIdx.x / PARTS;
-  const int p4 = (threadIdx.x % PARTS) * 4;
-  const bool mine = hh < nhc;
-  const int head = head0 + hh;
-  float mx = -INFINITY;
-  float L = 0.f;
-  f32x4 acc[NJ];
+// k_mla_lds: the small-grid form of k_mla_mfma (same work split: two wave pairs per
+// workgroup, each pair splitting every row by d; same exchange, softmax and merge). A lone
+// sequence's tile time is set by how many row-load instructions one CU issues, and a
+// register-operand load covers 16 rows x 64 bytes (16 half lines). Here each wave's rows go
+// straight to LDS (global_load_lds_dwordx4), 8 rows x one 128-byte line per instruction,
+// double-buffered: the next tile's loads are in flight while this tile's scores and P.V
+// read the staged rows. A 1 KiB block of 8 rows keeps 16-byte unit u of row r at slot
+// 8r + (u ^ r), so both the score operands (one row per lane) and the transposed value
+// reads spread over the banks. Rows past the context are zeroed in LDS before P.V (stale
+// cache bytes cannot turn 0 * v into NaN); their scores are masked as in k_mla_mfma.
+template <typename T, int DL, int DR>
+__global__ void __launch_bounds__(4 * kWave)
+k_mla_lds(MlaArgs a) {
+  using M = MlaMfma<T>;
+  using V8 = typename M::v8;
+  constexpr int NP = 2;
+  constexpr int LW = DL / 128;         // value lines (64 elements) per wave
+  constexpr int NV = 2 * LW;           // value chunks (32 elements) per wave
+  constexpr int NC = NV + 1;           // + the wave's rope chunk
+  constexpr int NDT = DL / 32;         // 16-wide d tiles of P.V per wave
+  static_assert(DL % 128 == 0 && DR == 64, "geometry");
+  constexpr int kRope = 2 * LW * 2 * 1024;           // rope blocks after the value blocks
+  constexpr int kWaveStage = kRope + 2 * 1024;       // one wave's rows of one tile
+  constexpr int kStageBytes = 2 * 2 * NP * kWaveStage;
+  constexpr int kXBytes = 2 * NP * 2 * kWave * 16;
+  constexpr int kCombineBytes = NP * 16 * 4 * 2 + NP * 16 * (DL + 4) * 4;
+  constexpr int kLoop = kStageBytes + kXBytes;
+  constexpr int kLdsBytes = kLoop > kCombineBytes ? kLoop : kCombineBytes;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pr = w >> 1;
+  const int hw = w & 1;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+
+  const int hc = blockIdx.x % a.hchunks;
+  const int b = blockIdx.x / a.hchunks;
+  const int split = blockIdx.y;
+  const int head0 = hc * 16;
+  const int nhc = min(16, a.nh - head0);
+
+  const int ctx = seq_context(a, b);
+  int t0, t1;
+  split_range(ctx, a.splits, split, t0, t1);
+  const int kend = min(t1 * kTile, ctx);
+
+  const int32_t* btrow = a.bt + b * a.bt_sb;
+  const int nloc = t1 > t0 + pr ? (t1 - t0 - pr + NP - 1) / NP : 0;
+  int blk_win = 0;
+  auto load_window = [&](int k0w) {
+    int hk = (t0 + pr + NP * (k0w + (lane >> 1))) * kTile + 16 * (lane & 1);
+    if (hk >= ctx) hk = (ctx - 1) & ~15;
+    if (hk < 0) hk = 0;
+    const int lb = static_cast<int>(a.bdiv.div(static_cast<uint32_t>(hk)));
+    blk_win = phys_block(a, btrow, lb);
+  };
+  // staged rows of tile buffer `buf` for this wave: value block (s, q, rb) = rows 8rb..8rb+7
+  // of half s, the wave's value line q; rope block s = the wave's rope chunk of half s
+  auto stage = [&](int buf) { return lds + (buf * 2 * NP + w) * kWaveStage; };
+  auto vblock = [&](int s, int q, int rb) { return ((s * LW + q) * 2 + rb) * 1024; };
+  const T* lat = static_cast<const T*>(a.lat);
+  auto load_tile = [&](int k, int buf) {
+    unsigned char* st = stage(buf);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (mine) {
-    float mw[NP];
+    for (int s = 0; s < 2; ++s) {
+      int hk0 = (t0 + pr + NP * k) * kTile + 16 * s;
+      if (hk0 >= ctx) hk0 = (ctx - 1) & ~15;
+      const int lb = static_cast<int>(a.bdiv.div(static_cast<uint32_t>(hk0)));
+      const int pb = __builtin_amdgcn_readlane(blk_win, ((k & 31) << 1) | s);
+      const T* rows = lat + pb * a.l_sblk + (hk0 - lb * a.block_size) * a.l_sslot;
+      const int rr = lane >> 3;
+      const int u = (lane & 7) ^ rr;
 #pragma unroll
-    for (int v = 0; v < NP; ++v) {
-      mw[v] = cb.m[v][hh];
-      mx = fmaxf(mx, mw[v]);
-    }
+      for (int q = 0; q < LW; ++q)
 #pragma unroll
-    for (int v = 0; v < NP; ++v) {
-      const float wt = mw[v] == -INFINITY ? 0.f : exp2_fast(mw[v] - mx);
-      L += wt * cb.l[v][hh];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        acc[j] += wt * *reinterpret_cast<const f32x4*>(&cb.o[v][hh][p4 + 4 * PARTS * j]);
-    }
-  }
-  T* orow = static_cast<T*>(a.out) + b * a.o_sb + head * a.o_sh + p4;
-  auto store_out = [&](float l) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      Pack<T, 4> r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) r.v[e] = from_f32<T>(acc[j][e] / l);
-      store_pack<T, 4>(orow + 4 * PARTS * j, r);
+        for (int rb = 0; rb < 2; ++rb)
+          load_to_lds16(rows + (8 * rb + rr) * a.l_sslot + (LW * hw + q) * 64 + 8 * u, st + vblock(s, q, rb));
+      load_to_lds16(rows + n * a.l_sslot + DL + 32 * hw + 8 * g, st + kRope + s * 1024);
     }
   };
-  if (a.splits == 1) {
-    if (mine) store_out(L);
-    return;
+  if (nloc > 0) {
+    load_window(0);
+    load_tile(0, 0);
   }
 
-  // Split-K: publish this split's partial with agent-coherent (sc1, written through) 16-byte
-  // stores, count the arrival once they have completed, and let the last split to arrive
-  // merge all of them with agent-coherent loads; it returns the counter to zero for the next
-  // launch. The workgroup's 16 partial rows of one split are contiguous, so one buffer
-  // resource (uniform base, exact size) addresses them.
-  const int64_t stride = int64_t(a.nseq) * a.nh;
-  const int64_t row0 = int64_t(b) * a.nh + head0;  // this chunk's first (sequence, head) row
-  if (mine) {
-    if (threadIdx.x % PARTS == 0) {
-      store_agent(a.part_m + split * stride + row0 + hh, mx);
-      store_agent(a.part_l + split * stride + row0 + hh, L);
-    }
-    const CoherentRsrc rs = coherent_rsrc(a.part_o + (split * stride + row0) * DL, nhc * DL);
+  // Q^T operand of this wave's chunks: value chunk j covers elements 64 (LW hw + j / 2) +
+  // 32 (j % 2) + 8g + [0, 8) of head n, the rope chunk DL + 32 hw + 8g + [0, 8).
+  V8 qv[NC];
+  {
+    const int hq = head0 + min(n, nhc - 1);
+    const T* qc = static_cast<const T*>(a.qc) + b * a.qc_sb + int64_t(hq) * a.qc_sh + 8 * g;
+    const T* qp = static_cast<const T*>(a.qpe) + b * a.qpe_sb + int64_t(hq) * a.qpe_sh + 8 * g;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      store_coherent<4>(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
+    for (int j = 0; j < NC; ++j) {
+      V8 v = __builtin_bit_cast(V8, j < NV ? load_pack<T, 8>(qc + 64 * (LW * hw + j / 2) + 32 * (j % 2))
+                                           : load_pack<T, 8>(qp + 32 * hw));
+      if (n >= nhc) v = V8{};
+      qv[j] = v;
+    }
   }
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __shared__ int is_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* cnt = a.counters + row0;
-    const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev == static_cast<uint32_t>(a.splits - 1);
-    if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!is_last) return;
 
-  // The merge. A head's threads share its splits for the max and the weights (thread p
-  // takes splits p, p + PARTS, ...; the weights go to LDS), then each thread sums its own d
-  // values over every split, four splits of loads in flight at a time.
-  const int pp = threadIdx.x % PARTS;
-  const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
-  float* wts = reinterpret_cast<float*>(lds);  // [16][splits]; the Combine area is free now
-  float gm = -INFINITY;
-  for (int sp = pp; sp < a.splits; sp += PARTS) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + row0 + hr));
+  float m = -INFINITY;
+  float lsum = 0.f;
+  f32x4 o[NDT];
 #pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gm = fmaxf(gm, shfl_xor_f(gm, k));
-  float gl = 0.f;
-  for (int sp = pp; sp < a.splits; sp += PARTS) {
-    const float ms = load_agent(a.part_m + sp * stride + row0 + hr);
-    const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
-    gl += wt * load_agent(a.part_l + sp * stride + row0 + hr);
-    wts[hh * a.splits + sp] = wt;
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  f32x4* xs = reinterpret_cast<f32x4*>(lds + kStageBytes);  // [wave][half][lane]
+  __shared__ unsigned sync_wr[NP * 2];
+  __shared__ unsigned sync_rd[NP * 2];
+  bool sync_ok = true;
+  auto pair_wait = [&](const unsigned* cnt, unsigned target) {
+    if (!sync_ok) return;
+    int spins = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSyncSpins) {
+        sync_ok = false;
+        if (lane == 0) atomicOr(a.err, EMBER_ERR_SYNC);
+        break;
+      }
+    }
+    asm volatile("" ::: "memory");
+  };
+  auto pair_post = [&](unsigned* cnt, unsigned v) {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    asm volatile("" ::: "memory");
+    __hip_atomic_store(cnt, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  if (threadIdx.x < NP * 2) {
+    sync_wr[threadIdx.x] = 0;
+    sync_rd[threadIdx.x] = 0;
   }
-#pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int roff = (hr * DL + p4) * int(sizeof(float));
-  constexpr int SB = 4;  // splits per batch of loads
-  int sp = 0;
-  for (; sp + SB <= a.splits; sp += SB) {
-    f32x4 v[SB][NJ];
-#pragma unroll
-    for (int u = 0; u < SB; ++u) {
-      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+
+  // per-lane parts of the staged-row addresses: score operands read row n of their half,
+  // value reads row 4g + n/4 of each half at d = 16 dt + 4 (n % 4)
+  const int srb = n >> 3, srr = n & 7;
+  const int vn = 4 * g + (n >> 2);
+  const int vrb = vn >> 3, vrr = vn & 7;
+
+  for (int k = 0; k < nloc; ++k) {
+    const int buf = k & 1;
+    const int k0 = (t0 + pr + NP * k) * kTile;
+    const bool partial = k0 + kTile > kend;
+    if (k + 1 < nloc) {
+      if (((k + 1) & 31) == 0) load_window(k + 1);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the other buffer's reads (tile k - 1) are done
+      asm volatile("" ::: "memory");
+      load_tile(k + 1, buf ^ 1);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt18);  // all but the 18 just issued: tile k is staged
+    } else {
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     }
+    asm volatile("" ::: "memory");
+    unsigned char* st = stage(buf);
+    if (partial) {
 #pragma unroll
-    for (int u = 0; u < SB; ++u) {
-      const float wt = wts[hh * a.splits + sp + u];
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[j] += wt * v[u][j];
+        for (int rb = 0; rb < 2; ++rb)
+          if (k0 + 16 * s + 8 * rb + (lane >> 3) >= kend)
+#pragma unroll
+            for (int q = 0; q < LW; ++q) store_pack<T, 8>(reinterpret_cast<T*>(st + vblock(s, q, rb)) + 8 * lane, Pack<T, 8>{});
+      asm volatile("" ::: "memory");
+    }
+
+    // partial scores over this wave's chunks
+    f32x4 sc[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      f32x4 c0 = f32x4{0.f, 0.f, 0.f, 0.f}, c1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const unsigned char* src =
+            j < NV ? st + vblock(s, j / 2, srb) + (8 * srr + ((4 * (j % 2) + g) ^ srr)) * 16
+                   : st + kRope + s * 1024 + 16 * lane;
+        const V8 kv = __builtin_bit_cast(V8, *reinterpret_cast<const Pack<T, 8>*>(src));
+        if (j % 2 == 0) c0 = M::run(kv, qv[j], c0);
+        else c1 = M::run(kv, qv[j], c1);
+      }
+      sc[s] = c0 + c1;
+    }
+    pair_wait(&sync_rd[w ^ 1], k);
+    xs[(w * 2 + 0) * kWave + lane] = sc[0];
+    xs[(w * 2 + 1) * kWave + lane] = sc[1];
+    pair_post(&sync_wr[w], k + 1);
+    pair_wait(&sync_wr[w ^ 1], k + 1);
+    sc[0] += xs[((w ^ 1) * 2 + 0) * kWave + lane];
+    sc[1] += xs[((w ^ 1) * 2 + 1) * kWave + lane];
+    pair_post(&sync_rd[w], k + 1);
+
+    float x[8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * s + i] = sc[s][i] * a.scale2;
+    if (partial) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (k0 + 16 * s + 4 * g + i >= kend) x[4 * s + i] = -INFINITY;
+    }
+    float mt = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, x[j]);
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    if (__any(mt > m + kLazy)) {
+      const float mn = fmaxf(m, mt);
+      const float alpha = exp2_fast(m - mn);
+      m = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+    }
+    V8 pb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float p = exp2_fast(x[j] - m);
+      lsum += p;
+      pb[j] = from_f32<T>(p);
+    }
+    constexpr int PVB = 8;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) v4s* lds_v4s;
+#pragma unroll
+    for (int d0 = 0; d0 < NDT; d0 += PVB) {
+      v8s va[PVB];
+#pragma unroll
+      for (int kk = 0; kk < PVB; ++kk) {
+        const int dt = d0 + kk;
+        const int slot = 8 * vrr + ((2 * (dt & 3) + ((n & 3) >> 1)) ^ vrr);
+        const unsigned char* lo_p = st + vblock(0, dt >> 2, vrb) + 16 * slot + 8 * (n & 1);
+        const unsigned char* hi_p = st + vblock(1, dt >> 2, vrb) + 16 * slot + 8 * (n & 1);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(reinterpret_cast<uintptr_t>(lo_p)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(reinterpret_cast<uintptr_t>(hi_p)));
+        va[kk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+#pragma unroll
+      for (int kk = 0; kk < PVB; ++kk) o[d0 + kk] = M::run(__builtin_bit_cast(V8, va[kk]), pb, o[d0 + kk]);
     }
   }
-  for (; sp < a.splits; ++sp) {
-    const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
-    const float wt = wts[hh * a.splits + sp];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
-  }
-  if (mine) store_out(gl);
+  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc);
 }
 
 constexpr int kAnyMaxD = 1024;          // DL + DR of the fp32 kernel
@@ -787,12 +1079,16 @@ int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_str
     const int ncu = device_cu_count();
     const bool small = ncu > 0 && progs * num_splits * 2 <= ncu;
     if (q_dtype == EMBER_F16) {
-      if (small)
+      if (small && kMlaStaged)
+        k_mla_lds<_Float16, kMlaDL, kMlaDR><<<grid, 4 * kWave, 0, st>>>(a);
+      else if (small)
         k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairsSmall, kMlaPairSync><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
       else
         k_mla_mfma<_Float16, kMlaDL, kMlaDR, kMlaPairs, kMlaPairSync><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
     } else {
-      if (small)
+      if (small && kMlaStaged)
+        k_mla_lds<__bf16, kMlaDL, kMlaDR><<<grid, 4 * kWave, 0, st>>>(a);
+      else if (small)
         k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairsSmall, kMlaPairSync><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
       else
         k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairs, kMlaPairSync><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
