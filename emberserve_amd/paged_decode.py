@@ -34,7 +34,7 @@ VARIANTS = ("sum", "dot")
 MAX_SPLITS = 32
 TILE = 32                 # keys per kernel tile
 MIN_KEYS_PER_SPLIT = 256
-LONG_SPLIT_KEYS = 1024    # keys per split at which MAX_SPLITS splits are allowed
+LONG_SPLIT_KEYS = 512     # keys per split at which MAX_SPLITS splits are allowed
 
 
 def interpreter_enabled() -> bool:
@@ -94,9 +94,9 @@ def default_num_splits(batch: int, num_kv_heads: int, max_context: int, device: 
     want = (target + programs // 2) // programs
     by_context = max(1, max_context // MIN_KEYS_PER_SPLIT)
     # The in-kernel merge grows with the split count: 32 splits pay only once every split
-    # holds >= 1024 keys (measured, B = 1, 32q/8kv x 128: ctx 8192 16 splits 28.8 us vs 32
-    # splits 37.8; ctx 16384 38.1 vs 43.2; ctx 32768 56.9 vs 53.9; 14q/2kv x 64 at 8192:
-    # 16.6 vs 21.5).
+    # holds >= 512 keys (measured, B = 1, 32q/8kv x 128, splits 16 / 32: ctx 8192 16.7 /
+    # 17.4 us; ctx 16384 25.0 / 22.9; ctx 32768 41.7 / 33.5; 40-64 splits were slower than
+    # 32 up to 65536 keys).
     cap = MAX_SPLITS if max_context >= MAX_SPLITS * LONG_SPLIT_KEYS else MAX_SPLITS // 2
     return max(1, min(cap, want, by_context))
 

@@ -246,7 +246,8 @@ def test_paged_decode_default_splits_follow_the_grid_rule(monkeypatch):
     assert pd.default_num_splits(8, 8, 8192, dev, 32, 128) == 4        # 64 programs -> 256
     assert pd.default_num_splits(128, 2, 8192, dev, 14, 64) == 1       # 256 programs
     assert pd.default_num_splits(32, 2, 2048, dev, 14, 64) == 4        # 64 programs -> 256
-    assert pd.default_num_splits(1, 8, 8192, dev, 32, 128) == 16       # < 1024 keys per split at 32
+    assert pd.default_num_splits(1, 8, 8192, dev, 32, 128) == 16       # < 512 keys per split at 32
+    assert pd.default_num_splits(1, 8, 16384, dev, 32, 128) == 32      # 512 keys per split at 32
     assert pd.default_num_splits(1, 8, 32768, dev, 32, 128) == 32      # capped at MAX_SPLITS
     assert pd.default_num_splits(1, 2, 8192, dev, 14, 64) == 16
     assert pd.default_num_splits(1, 8, 512, dev, 32, 128) == 2         # >= 256 keys per split
