@@ -247,12 +247,29 @@ k_decode_mfma(DecodeArgs a) {
   // V[16r + 4g + jj][16dt + n] for jj < 4: the A operand's kslots 8g + 4r + jj.
   const T* vtr = vl + (4 * g + (n >> 2)) * VS + 4 * (n & 3);
 
-  // Loads of one chunk (KT tiles from tile tc): a half past the context still loads (from
-  // the last valid half's block) so the loads stay unconditional; keys past the split's
-  // range are masked after the scores.
+  // The wave's physical block ids, a window of WIN chunks at a time: lane 2(KT kk + u) + s
+  // holds the block of half s of tile u of the wave's chunk kk of the window, so a chunk's
+  // row loads never wait on a block-table read (one table read per WIN chunks instead of
+  // one per chunk, which at a single sequence put two dependent round trips on every
+  // chunk). Halves past the context point at the last valid half's block, as the row loads
+  // below do; a wave without tiles reads no table entry.
+  constexpr int WIN = kWave / (2 * KT);
+  int blk_win = 0;
+  auto load_window = [&](int k0w) {
+    const int slot = lane >> 1;
+    int hk = (t0 + KT * w + CH * (k0w + slot / KT) + slot % KT) * kTile + 16 * (lane & 1);
+    if (hk >= ctx) hk = (ctx - 1) & ~15;
+    if (hk < 0) hk = 0;
+    const int lb = static_cast<int>(a.bdiv.div(static_cast<uint32_t>(hk)));
+    blk_win = phys_block(a, btrow, lb);
+  };
+
+  // Loads of the wave's chunk k (KT tiles from tile tc): a half past the context still
+  // loads (from the last valid half's block) so the loads stay unconditional; keys past the
+  // split's range are masked after the scores.
   Pack<T, 8> kr[KT][2][NP];
   Pack<T, 8> vr[KT][2][NP];
-  auto load_chunk = [&](int tc) {
+  auto load_chunk = [&](int tc, int k) {
 #pragma unroll
     for (int u = 0; u < KT; ++u)
 #pragma unroll
@@ -260,7 +277,7 @@ k_decode_mfma(DecodeArgs a) {
         int hk0 = (tc + u) * kTile + 16 * s;
         if (hk0 >= ctx) hk0 = (ctx - 1) & ~15;
         const int lb = static_cast<int>(a.bdiv.div(static_cast<uint32_t>(hk0)));
-        const int pb = phys_block(a, btrow, lb);
+        const int pb = __builtin_amdgcn_readlane(blk_win, (((k % WIN) * KT + u) << 1) | s);
         const int slot = hk0 - lb * a.block_size + n;
         const T* kp = kbase + pb * a.k_sblk + slot * a.k_sslot;
         const T* vp = vbase + pb * a.v_sblk + slot * a.v_sslot;
@@ -272,9 +289,16 @@ k_decode_mfma(DecodeArgs a) {
   };
 
   int tc = t0 + KT * w;
-  if (PF && tc < t1) load_chunk(tc);
-  for (; tc < t1; tc += CH) {
-    if (!PF) load_chunk(tc);
+  int kc = 0;  // the wave's chunk index
+  if (tc < t1) {
+    load_window(0);
+    if (PF) load_chunk(tc, 0);
+  }
+  for (; tc < t1; tc += CH, ++kc) {
+    if (!PF) {
+      if (kc > 0 && kc % WIN == 0) load_window(kc);
+      load_chunk(tc, kc);
+    }
     const int k0 = tc * kTile;
     const bool partial = k0 + KT * kTile > kend;  // wave-uniform
 
@@ -309,7 +333,10 @@ k_decode_mfma(DecodeArgs a) {
     asm volatile("" ::: "memory");
     // K and V of this chunk are consumed (scores issued, V in LDS): the registers take the
     // wave's next chunk while this one's softmax and P.V run.
-    if (PF && tc + CH < t1) load_chunk(tc + CH);
+    if (PF && tc + CH < t1) {
+      if ((kc + 1) % WIN == 0) load_window(kc + 1);
+      load_chunk(tc + CH, kc + 1);
+    }
 
     float x[KT][8];
 #pragma unroll

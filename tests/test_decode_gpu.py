@@ -61,9 +61,11 @@ def _to_dev(*ts):
     return [t.to(DEV) for t in ts]
 
 
-def _check(got: torch.Tensor, q, kc, vc, bt, ctx, scale, mfma: bool, what: str) -> None:
-    o = ref.paged_decode(q.float(), kc, vc, bt, ctx, scale)
-    mass = ref.paged_decode_prob_mass(q.float(), kc, vc, bt, ctx, scale)
+def _check(got: torch.Tensor, q, kc, vc, bt, ctx, scale, mfma: bool, what: str, want=None) -> None:
+    """`want` = (output, probability mass) from the oracle, when the caller reuses them."""
+    if want is None:
+        want = _want(q, kc, vc, bt, ctx, scale)
+    o, mass = want
     u_out = U[q.dtype]
     if mfma:
         u_p = U[kc.dtype]
@@ -75,6 +77,11 @@ def _check(got: torch.Tensor, q, kc, vc, bt, ctx, scale, mfma: bool, what: str) 
     assert not bool(bad.any()), (
         f"{what}: {int(bad.sum())} of {err.numel()} elements out of tolerance; "
         f"max err {float(err.max()):.3e}, worst ratio {float((err / tol).max()):.2f}")
+
+
+def _want(q, kc, vc, bt, ctx, scale):
+    return (ref.paged_decode(q.float(), kc, vc, bt, ctx, scale),
+            ref.paged_decode_prob_mass(q.float(), kc, vc, bt, ctx, scale))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -187,6 +194,24 @@ def test_decode_qwen3_small_and_full_grids(batch):
         _say(f"decode qwen3 B={batch} splits={splits}")
         got = paged_attention_decode(dq, dkc, dvc, dbt, dcl, 128 ** -0.5, num_splits=splits)
         _check(got, q, kc, vc, bt, cl, 128 ** -0.5, True, f"B={batch} splits={splits}")
+    assert _lib.read_errors() == 0
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,block", [(14, 2, 64, torch.float16, 16), (32, 8, 128, torch.bfloat16, 16),
+                                                   (32, 8, 128, torch.bfloat16, 256)])
+def test_decode_long_contexts_cross_block_id_windows(hq, hkv, d, dtype, block):
+    """Each wave keeps the block ids of its next 32 key tiles in a register window and
+    rereads the table every 32 tiles. One split over 20000 keys gives every wave 79 (8
+    waves) or 157 (4 waves) tiles, so several windows; 3 splits and a 9001-key sequence
+    move the window edges, and a 1-key sequence sits beside them."""
+    ctx = [20000, 9001, 1]
+    q, kc, vc, bt, cl = gen.decode_inputs(ctx, hq, hkv, d, block, dtype, seed=hq + block)
+    dq, dkc, dvc, dbt, dcl = _to_dev(q, kc, vc, bt, cl)
+    want = _want(q, kc, vc, bt, cl, d ** -0.5)
+    for splits in (1, 3):
+        _say(f"decode long contexts {hq}q/{hkv}kv d{d} block {block} splits={splits}")
+        got = paged_attention_decode(dq, dkc, dvc, dbt, dcl, d ** -0.5, num_splits=splits)
+        _check(got, q, kc, vc, bt, cl, d ** -0.5, True, f"splits={splits}", want)
     assert _lib.read_errors() == 0
 
 
