@@ -282,51 +282,50 @@ __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds,
   __syncthreads();
   if (!is_last) return;
 
-  // The merge. A head's threads share its splits for the max and the weights (thread p
-  // takes splits p, p + PARTS, ...; the weights go to LDS), then each thread sums its own d
-  // values over every split, four splits of loads in flight at a time.
-  const int pp = threadIdx.x % PARTS;
+  // The merge, online over chunks of kMergeChunk splits: each thread issues every load of a
+  // chunk at once (the splits' max and sum of its head, its own d values of each split's
+  // partial), so a chunk costs one round trip. The running max moves per chunk.
   const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
-  float* wts = reinterpret_cast<float*>(lds);  // [16][splits]; the Combine area is free now
+  const int roff = (hr * DL + p4) * int(sizeof(float));
+  constexpr int kMergeChunk = NJ >= 8 ? 4 : 8;  // registers: kMergeChunk x (4 NJ + 2)
   float gm = -INFINITY;
-  for (int sp = pp; sp < a.splits; sp += PARTS) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + row0 + hr));
-#pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gm = fmaxf(gm, shfl_xor_f(gm, k));
   float gl = 0.f;
-  for (int sp = pp; sp < a.splits; sp += PARTS) {
-    const float ms = load_agent(a.part_m + sp * stride + row0 + hr);
-    const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
-    gl += wt * load_agent(a.part_l + sp * stride + row0 + hr);
-    wts[hh * a.splits + sp] = wt;
-  }
-#pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
-  __syncthreads();
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int roff = (hr * DL + p4) * int(sizeof(float));
-  constexpr int SB = 4;  // splits per batch of loads
-  int sp = 0;
-  for (; sp + SB <= a.splits; sp += SB) {
-    f32x4 v[SB][NJ];
+  for (int c0 = 0; c0 < a.splits; c0 += kMergeChunk) {
+    const int cn = min(kMergeChunk, a.splits - c0);
+    float ms[kMergeChunk], ls[kMergeChunk];
+    f32x4 v[kMergeChunk][NJ];
 #pragma unroll
-    for (int u = 0; u < SB; ++u) {
-      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((sp + u) * stride + row0) * DL, nhc * DL);
+    for (int u = 0; u < kMergeChunk; ++u) {
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+      for (int j = 0; j < NJ; ++j) v[u][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (u < cn) {  // uniform
+        const int sp = c0 + u;
+        ms[u] = load_agent(a.part_m + sp * stride + row0 + hr);
+        ls[u] = load_agent(a.part_l + sp * stride + row0 + hr);
+        const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+      }
     }
+    float cm = gm;
 #pragma unroll
-    for (int u = 0; u < SB; ++u) {
-      const float wt = wts[hh * a.splits + sp + u];
+    for (int u = 0; u < kMergeChunk; ++u) cm = fmaxf(cm, ms[u]);
+    const float alpha = gm == -INFINITY ? 0.f : exp2_fast(gm - cm);
+    gl *= alpha;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) {
+      const float wt = ms[u] == -INFINITY ? 0.f : exp2_fast(ms[u] - cm);
+      gl += wt * ls[u];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) acc[j] += wt * v[u][j];
     }
-  }
-  for (; sp < a.splits; ++sp) {
-    const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * DL, nhc * DL);
-    const float wt = wts[hh * a.splits + sp];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<4>(rs, roff + 4 * PARTS * j * int(sizeof(float)));
+    gm = cm;
   }
   if (mine) store_out(gl);
 }

@@ -489,60 +489,56 @@ k_decode_mfma(DecodeArgs a) {
   __syncthreads();
   if (!is_last) return;
 
-  // The merge. The global max: a head's threads share its splits (thread p takes splits
-  // p, p + PARTS, ...). Then, per chunk of kWtChunk splits, the weights go to LDS
-  // (split-parallel again) and every thread sums its own d values over the chunk's
-  // splits, four splits of loads in flight at a time.
-  const int pp = threadIdx.x % PARTS;
+  // The merge, online over chunks of kMergeChunk splits: each thread issues every load of a
+  // chunk at once (the splits' max and sum of its head, its own d values of each split's
+  // partial), so a chunk costs one round trip. The running max moves per chunk; with one
+  // chunk the sums are formed in the same order as a two-pass merge.
   const int hr = min(hh, nhc - 1);  // padded heads read a real row and store nothing
+  const int roff = (hr * D + pv) * int(sizeof(float));
+  // 8 splits per chunk: a 16-split chunk's registers (16 x (2 + floats per split)) raised
+  // the D = 64 kernel from 97 to 141 VGPRs and cut its occupancy (B = 128 x 2048 at 32
+  // splits: 75.5 -> 126.6 us)
+  constexpr int kMergeChunk = 8;
   float gm = -INFINITY;
-  for (int sp = pp; sp < a.splits; sp += PARTS) gm = fmaxf(gm, load_agent(a.part_m + sp * stride + row0 + hr));
-#pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gm = fmaxf(gm, shfl_xor_f(gm, k));
-  constexpr int kWtChunk = 128;
-  static_assert(16 * kWtChunk * int(sizeof(float)) <= kLdsBytes, "weights chunk");
-  float* wts = reinterpret_cast<float*>(lds);  // [16][kWtChunk]; the Combine area is free now
   float gl = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = FV{};
-  const int roff = (hr * D + pv) * int(sizeof(float));
-  for (int c0 = 0; c0 < a.splits; c0 += kWtChunk) {
-    const int cn = min(kWtChunk, a.splits - c0);
-    __syncthreads();  // the previous chunk's weights are consumed
-    for (int u = pp; u < cn; u += PARTS) {
-      const int64_t r = (c0 + u) * stride + row0 + hr;
-      const float ms = load_agent(a.part_m + r);
-      const float wt = ms == -INFINITY ? 0.f : exp2_fast(ms - gm);
-      gl += wt * load_agent(a.part_l + r);
-      wts[hh * kWtChunk + u] = wt;
-    }
-    __syncthreads();
-    constexpr int SB = 4;  // splits per batch of loads
-    int u = 0;
-    for (; u + SB <= cn; u += SB) {
-      FV v[SB][NJ];
+  for (int c0 = 0; c0 < a.splits; c0 += kMergeChunk) {
+    const int cn = min(kMergeChunk, a.splits - c0);
+    float ms[kMergeChunk], ls[kMergeChunk];
+    FV v[kMergeChunk][NJ];
 #pragma unroll
-      for (int q = 0; q < SB; ++q) {
-        const CoherentRsrc rs = coherent_rsrc(a.part_o + ((c0 + u + q) * stride + row0) * D, nhc * D);
+    for (int u = 0; u < kMergeChunk; ++u) {
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) v[q][j] = load_coherent<VEC>(rs, roff + VEC * PARTS * j * int(sizeof(float)));
-      }
+      for (int j = 0; j < NJ; ++j) v[u][j] = FV{};
+      if (u < cn) {  // uniform
+        const int sp = c0 + u;
+        const int64_t r = sp * stride + row0 + hr;
+        ms[u] = load_agent(a.part_m + r);
+        ls[u] = load_agent(a.part_l + r);
+        const CoherentRsrc rs = coherent_rsrc(a.part_o + (sp * stride + row0) * D, nhc * D);
 #pragma unroll
-      for (int q = 0; q < SB; ++q) {
-        const float wt = wts[hh * kWtChunk + u + q];
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[j] += wt * v[q][j];
+        for (int j = 0; j < NJ; ++j) v[u][j] = load_coherent<VEC>(rs, roff + VEC * PARTS * j * int(sizeof(float)));
       }
     }
-    for (; u < cn; ++u) {
-      const CoherentRsrc rs = coherent_rsrc(a.part_o + ((c0 + u) * stride + row0) * D, nhc * D);
-      const float wt = wts[hh * kWtChunk + u];
+    float cm = gm;
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[j] += wt * load_coherent<VEC>(rs, roff + VEC * PARTS * j * int(sizeof(float)));
+    for (int u = 0; u < kMergeChunk; ++u) cm = fmaxf(cm, ms[u]);
+    const float alpha = gm == -INFINITY ? 0.f : exp2_fast(gm - cm);
+    gl *= alpha;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+#pragma unroll
+    for (int u = 0; u < kMergeChunk; ++u) {
+      const float wt = ms[u] == -INFINITY ? 0.f : exp2_fast(ms[u] - cm);
+      gl += wt * ls[u];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] += wt * v[u][j];
     }
+    gm = cm;
   }
-#pragma unroll
-  for (int k = 1; k < PARTS; k <<= 1) gl += shfl_xor_f(gl, k);
   if (mine) store_out(gl);
 }
 
