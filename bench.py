@@ -358,6 +358,22 @@ def _ops(torch, ops, tables):
                       nbytes, make, lambda a: mla_decode_hip(a[0], a[1], a[2], a[3], 192 ** -0.5, dl),
                       lat_bytes, cpu=("mla_decode", (b, ctx)) if cpu else None))
 
+    def gate_up(cfg, t, hidden, inter, label):
+        """The dense MLP's gate_up projection + silu_and_mul (qwen2.py:60-61) at a decode
+        batch: the fused kernel and the unfused pair (torch linear = hipBLASLt, then
+        silu_and_mul) on the same inputs."""
+        from emberserve_amd.gate_up_silu import gate_up_silu, gate_up_silu_torch
+        wbytes = 2 * inter * hidden * 2
+
+        def make(i):
+            return (randn((t, hidden), bf, 270 + i), randn((2 * inter, hidden), bf, 280 + i, std=hidden ** -0.5))
+        nbytes = wbytes + t * hidden * 2 + t * inter * 2
+        shape = f"{label}: x[{t},{hidden}] w[{2 * inter},{hidden}] bf16"
+        out.append(Op("gate_up_silu", cfg, shape, nbytes, make,
+                      lambda a: gate_up_silu(a[0], a[1], fused=True), wbytes))
+        out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
+                      lambda a: gate_up_silu_torch(a[0], a[1]), wbytes))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -398,6 +414,10 @@ def _ops(torch, ops, tables):
     mla_decode("mla", 128, 320, "moonlight")
     mla_decode("mla", 32, 4096, "moonlight", cpu=False)
     mla_decode("mla", 256, 2048, "moonlight", cpu=False)
+    # SiLU-mul in the gate_up projection's epilogue (qwen2.py:60-61) at decode batches.
+    for t in (1, 16):
+        gate_up("mlp", t, 4096, 12288, "qwen3-8b")
+        gate_up("mlp", t, 3584, 18944, "qwen2.5-7b")
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
     # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -62,13 +62,16 @@ SIGNATURES: dict[str, list] = {
     "ember_mla_decode_workspace_bytes": [_i64, _i64, _i64, _i64],
     "ember_mla_decode": [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                          _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _p, _i64, _p, _i64, _i64, _p],
+    "ember_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],
+    "ember_gate_up_silu": [_p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],
 }
 
 _RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspace_bytes": ctypes.c_int64,
-            "ember_mla_decode_workspace_bytes": ctypes.c_int64}
+            "ember_mla_decode_workspace_bytes": ctypes.c_int64,
+            "ember_gate_up_silu_workspace_bytes": ctypes.c_int64}
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:

@@ -1,0 +1,442 @@
+// The dense MLP's gate_up projection with SiLU-and-mul as its epilogue, for decode-sized
+// batches (T <= 64 tokens) on gfx950.
+//
+// Reference: Qwen2MLP.forward (emberserve/model/qwen2.py:60-61),
+//   silu_and_mul(gate_up_proj(x)),  gate_up_proj = nn.Linear(H, 2I, bias=False),
+// weight rows [0, I) gate and [I, 2I) up (qwen2.py:49-57), then ops.silu_and_mul
+// (ops.py:84-87). The linear layer's output is rounded to the activation dtype before the
+// activation reads it, so per output element
+//   g = round(x . W[j]),  u = round(x . W[I + j]),  out[t, j] = round(round(silu(g)) * u)
+// with fp32 dot products (MFMA accumulation; the order of the k terms is this kernel's
+// own, so results agree with another GEMM to within the dot product's rounding).
+//
+// Why a kernel of its own: at T <= 64 the projection is a stream over the weights
+// (2 I H elements, 201 MB at Qwen3-8B) and the unfused pair also writes and rereads the
+// [T, 2I] projection and pays a second launch. The library GEMM streams the weights at
+// 4.3-5.2 TB/s at these sizes.
+//
+// Work split. The work is (slab, k step) units: a slab is 64 output columns (wave w of a
+// workgroup: gate rows 16w.. and the matching up rows, so the epilogue pairs them in
+// registers), a k step 64 elements of H. A persistent grid (one or two workgroups per CU)
+// takes equal contiguous runs of the slab-major unit order, so every CU streams the same
+// number of weight bytes and its load ring runs on across slab boundaries. Per unit every
+// wave moves its 32 weight rows, and the workgroup the unit's x rows, straight from HBM to
+// LDS (global_load_lds_dwordx4: 8 rows x one 128-byte line per instruction, the cheapest
+// load issue per byte on a CU) in a ring of NS stages, then forms D[weight row][token] with
+// v_mfma_f32_16x16x32 (A = weight rows, B = tokens). A 1 KiB LDS block of 8 rows keeps
+// 16-byte unit c of row r at slot 8r + (c ^ r), so the operand reads (one row per lane)
+// spread over the banks.
+//
+// A workgroup that covers a slab's whole k range writes its output directly. Otherwise each
+// workgroup that covers part of it leaves an agent-coherent partial; at the end of its run a
+// workgroup counts its partials in (one per-slab arrival counter) and the last to arrive
+// sums the slab's partials in k order (so results do not depend on arrival order), applies
+// the epilogue and returns the counter to zero for the next launch.
+#include <algorithm>
+
+#include "ember_common.h"
+
+#ifndef EMBER_GU_STAGES
+#define EMBER_GU_STAGES 3
+#endif
+// token tiles (of 16) up to which every wave loads its own copy of x
+#ifndef EMBER_GU_PRIVX_MT
+#define EMBER_GU_PRIVX_MT 2
+#endif
+
+namespace ember {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct GuMfma;
+template <>
+struct GuMfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct GuMfma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kGuWaves = 4;
+constexpr int kGuRows = 16;                   // gate (and up) rows per wave
+constexpr int kGuSlab = kGuWaves * kGuRows;   // output columns per workgroup
+constexpr int kGuBK = 64;                     // k per stage: one 128-byte line per row
+constexpr int kGuMaxTokens = 64;
+
+struct GuArgs {
+  const void* x;
+  int64_t xs;
+  const void* w;
+  int64_t ws;
+  void* out;
+  int64_t os;
+  int T, H, I;
+  int64_t max_parts;  // partial slots per slab
+  float* part;
+  uint32_t* counters;
+};
+
+// One 16-byte-per-lane load from global memory straight to LDS: lane i's 16 bytes land at
+// lds_base + 16 i. Only the device pass sees the builtin (the host pass drops the kernel's
+// launch stub when it appears in a kernel body it does not generate code for).
+__device__ __forceinline__ void gu_load_lds16(const void* gptr, void* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)(
+                                             reinterpret_cast<uintptr_t>(lds_base)), 16, 0, 0);
+#else
+  (void)gptr;
+  (void)lds_base;
+#endif
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding, expcnt and lgkmcnt left alone).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup b's units are [start(b), start(b + 1)), start(b) = floor(b total / G); the
+// workgroup that holds unit u is floor(((u + 1) G - 1) / total).
+__device__ __host__ __forceinline__ int64_t gu_start(int64_t b, int64_t total, int64_t G) { return b * total / G; }
+__device__ __host__ __forceinline__ int64_t gu_owner(int64_t u, int64_t total, int64_t G) {
+  return ((u + 1) * G - 1) / total;
+}
+
+// A workgroup barrier that waits for this wave's LDS reads but not for its global loads
+// (__syncthreads() carries a workgroup fence, which waits for every outstanding load and
+// would drain the load ring each step). The asm clobbers keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void gu_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Slabs a run leaves partials for: only its first and last (it emits every slab it covers
+// whole), so two.
+constexpr int kGuMaxFlush = 2;
+
+// PRIVX: every wave loads its own copy of a step's x rows (2 KiB per 16 tokens, from L2),
+// so the waves never wait for each other; otherwise the four waves share one copy and
+// meet at a barrier every step. Private copies cost XB load instructions per wave per
+// step, affordable for up to 32 tokens.
+template <typename T, int MT, int NS, bool PRIVX>
+__global__ void __launch_bounds__(kGuWaves * kWave, 1)
+k_gate_up_silu(GuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  constexpr int XB = 2 * MT;                                // 8-token blocks of x per stage
+  constexpr int XBW = PRIVX ? XB : (XB + kGuWaves - 1) / kGuWaves;  // x blocks each wave loads
+  constexpr int WB = 4;                                     // weight blocks per wave per stage
+  constexpr int WBYTES = kGuWaves * WB * 1024;
+  constexpr int STAGE = WBYTES + (PRIVX ? kGuWaves : 1) * XB * 1024;
+  constexpr int LPS = WB + XBW;                             // direct loads per wave per stage
+  constexpr int kFloats = kGuWaves * MT * 2 * kWave * 4;    // one partial of a slab
+  static_assert(NS >= 2 && NS <= 4 && LPS * (NS - 1) < 64, "stages");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NS * STAGE];
+  __shared__ int last_flags[kGuMaxFlush];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int64_t nk = a.H / kGuBK;                 // k steps per slab
+  const int64_t total = static_cast<int64_t>(a.I / kGuSlab) * nk;
+  const int64_t G = gridDim.x;
+  const int64_t u0 = gu_start(blockIdx.x, total, G);
+  const int nu = static_cast<int>(gu_start(blockIdx.x + 1, total, G) - u0);  // >= 1 (G <= total)
+
+  // Direct-load lanes: lane l moves row l / 8 of an 8-row block, global 16-byte unit
+  // (l % 8) ^ (l / 8), into slot l of the block.
+  const int lr = lane >> 3;
+  const int lc = (lane & 7) ^ lr;
+  const T* xg = static_cast<const T*>(a.x);
+  const T* wg = static_cast<const T*>(a.w);
+  int64_t wrow[WB];  // element offsets of this lane's weight rows in slab 0
+#pragma unroll
+  for (int q = 0; q < WB; ++q)
+    wrow[q] = static_cast<int64_t>((q < 2 ? 0 : a.I) + w * kGuRows + 8 * (q & 1) + lr) * a.ws + 8 * lc;
+  const int64_t slab_stride = static_cast<int64_t>(kGuSlab) * a.ws;
+  const T* xsrc[XBW];
+  int xdst[XBW];
+#pragma unroll
+  for (int j = 0; j < XBW; ++j) {
+    // shared: past the last block a wave loads it again (identical bytes)
+    const int blk = PRIVX ? j : min(w + kGuWaves * j, XB - 1);
+    const int tok = min(8 * blk + lr, a.T - 1);  // padded tokens read the last real one
+    xsrc[j] = xg + static_cast<int64_t>(tok) * a.xs + 8 * lc;
+    xdst[j] = WBYTES + (PRIVX ? w * XB * 1024 : 0) + blk * 1024;
+  }
+  // The issue position walks the units in order: (slab, k step) of the next unit to load.
+  int64_t is_slab = u0 / nk;
+  int64_t is_k = u0 - is_slab * nk;
+  auto issue = [&](int j) {
+    unsigned char* st = lds + (j % NS) * STAGE;
+    const int64_t kk = is_k * kGuBK;
+    const T* wbase = wg + is_slab * slab_stride + kk;
+#pragma unroll
+    for (int q = 0; q < WB; ++q) gu_load_lds16(wbase + wrow[q], st + (w * WB + q) * 1024);
+#pragma unroll
+    for (int jx = 0; jx < XBW; ++jx) gu_load_lds16(xsrc[jx] + kk, st + xdst[jx]);
+    if (++is_k == nk) {
+      is_k = 0;
+      ++is_slab;
+    }
+  };
+
+  f32x4 acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Operand slots: lane (n, g) reads row n of a 16-row pair of blocks, unit 4h + g (k half h).
+  auto slot = [&](int h) {
+    const int r = n & 7;
+    return (n >> 3) * 1024 + (8 * r + (((4 * h + g) ^ r) & 7)) * 16;
+  };
+  auto compute = [&](int j) {
+    const unsigned char* st = lds + (j % NS) * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int so = slot(h);
+      const V8 wgate = *reinterpret_cast<const V8*>(st + (w * WB) * 1024 + so);
+      const V8 wup = *reinterpret_cast<const V8*>(st + (w * WB + 2) * 1024 + so);
+      V8 xv[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xv[mt] = *reinterpret_cast<const V8*>(st + WBYTES + (PRIVX ? w * XB * 1024 : 0) + 2 * mt * 1024 + so);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] = M::run(wgate, xv[mt], acc[mt][0]);
+        acc[mt][1] = M::run(wup, xv[mt], acc[mt][1]);
+      }
+    }
+  };
+
+  // Epilogue of slab `sl` from sums `v`: lane (n, g) holds D[row 4g + i][token 16 mt + n]
+  // of its wave's gate and up tiles, so output columns sl * 64 + 16 w + 4g + [0, 4).
+  T* out = static_cast<T*>(a.out);
+  auto emit = [&](int64_t sl, const f32x4 (&v)[MT][2]) {
+    const int64_t col = sl * kGuSlab + w * kGuRows + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int tok = 16 * mt + n;
+      if (tok < a.T) {
+        Pack<T, 4> o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gf = round_to<T>(v[mt][0][i]);
+          const float uf = round_to<T>(v[mt][1][i]);
+          const float act = round_to<T>(gf / (1.0f + expf(-gf)));
+          o.v[i] = from_f32<T>(act * uf);
+        }
+        store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
+      }
+    }
+  };
+  // Where a slab's partials live: part p of slab sl (p = contributing workgroup's order).
+  auto part_rsrc = [&](int64_t sl, int64_t p) {
+    return coherent_rsrc(a.part + (sl * a.max_parts + p) * kFloats, kFloats);
+  };
+  auto part_off = [&](int mt, int gu) { return (((w * MT + mt) * 2 + gu) * kWave + lane) * 16; };
+
+  int64_t flushed[kGuMaxFlush];
+  int nflush = 0;
+  int64_t cur_slab = u0 / nk;
+  int64_t cur_k = u0 - cur_slab * nk;
+  int64_t cur_first = cur_k;  // first k step of the current slab in this run
+
+  // The ring: loads of unit j + NS - 1 are issued once every wave is past unit j - 1 (whose
+  // buffer they overwrite). Each wave waits for its own loads of a unit, then the barrier
+  // makes every wave's loads of it visible.
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j)
+    if (j < nu) issue(j);
+  for (int j = 0; j < nu; ++j) {
+    const int ahead = min(NS - 2, nu - 1 - j);  // units issued past this one
+    if (ahead >= 2) wait_vm<2 * LPS>();
+    else if (ahead == 1) wait_vm<LPS>();
+    else wait_vm<0>();
+    if constexpr (PRIVX) {
+      asm volatile("" ::: "memory");  // this wave's reads of the buffer it refills are done
+    } else {
+      gu_barrier();
+    }
+    if (j + NS - 1 < nu) issue(j + NS - 1);
+    compute(j);
+    const bool slab_end = cur_k == nk - 1 || j == nu - 1;
+    if (slab_end) {
+      if (cur_first == 0 && cur_k == nk - 1) {
+        emit(cur_slab, acc);  // the whole k range of this slab is here
+      } else {
+        const int64_t p = gu_owner(cur_slab * nk + cur_first, total, G) -
+                          gu_owner(cur_slab * nk, total, G);
+        const CoherentRsrc rs = part_rsrc(cur_slab, p);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int gu = 0; gu < 2; ++gu) store_coherent<4>(rs, part_off(mt, gu), acc[mt][gu]);
+        if (nflush < kGuMaxFlush) flushed[nflush++] = cur_slab;
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ++cur_slab;
+      cur_k = 0;
+      cur_first = 0;
+    } else {
+      ++cur_k;
+    }
+  }
+  if (nflush == 0) return;
+
+  // Count this workgroup's partials in; the last contributor of a slab merges it.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x < nflush) {
+    const int64_t sl = flushed[threadIdx.x];
+    const uint32_t parts =
+        static_cast<uint32_t>(gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1);
+    uint32_t* cnt = a.counters + sl;
+    const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == parts - 1;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flags[threadIdx.x] = last;
+  }
+  __syncthreads();
+  for (int f = 0; f < nflush; ++f) {
+    if (!last_flags[f]) continue;  // uniform
+    const int64_t sl = flushed[f];
+    const int64_t parts = gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1;
+    f32x4 sum[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sum[mt][0] = sum[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    constexpr int SB = 4;  // partials per batch of loads
+    for (int64_t p0 = 0; p0 < parts; p0 += SB) {
+      f32x4 v[SB][MT][2];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const CoherentRsrc rs = part_rsrc(sl, min<int64_t>(p0 + u, parts - 1));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int gu = 0; gu < 2; ++gu)
+            v[u][mt][gu] = p0 + u < parts ? load_coherent<4>(rs, part_off(mt, gu)) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int gu = 0; gu < 2; ++gu) sum[mt][gu] += v[u][mt][gu];
+    }
+    emit(sl, sum);
+  }
+}
+
+template <typename T, int MT>
+int launch_gu(const GuArgs& a, int64_t programs, hipStream_t st) {
+  hipLaunchKernelGGL((k_gate_up_silu<T, MT, EMBER_GU_STAGES, (MT <= EMBER_GU_PRIVX_MT)>),
+                     dim3(static_cast<uint32_t>(programs)), dim3(kGuWaves * kWave), 0, st, a);
+  return launch_status();
+}
+
+template <typename T>
+int launch_gu_typed(const GuArgs& a, int64_t programs, hipStream_t st) {
+  switch ((a.T + 15) / 16) {
+    case 1: return launch_gu<T, 1>(a, programs, st);
+    case 2: return launch_gu<T, 2>(a, programs, st);
+    case 3: return launch_gu<T, 3>(a, programs, st);
+    case 4: return launch_gu<T, 4>(a, programs, st);
+    default: return EMBER_EINVAL;
+  }
+}
+
+int64_t gu_partial_floats(int64_t tokens) {
+  const int64_t mt = (tokens + 15) / 16;
+  return kGuWaves * mt * 2 * kWave * 4;
+}
+
+// The plan of a launch: workgroups G (at most one per unit) and the most workgroups that
+// share one slab (the partial slots per slab).
+struct GuPlan {
+  int64_t programs = 0, max_parts = 0;
+};
+
+GuPlan gu_plan(int64_t hidden, int64_t inter, int64_t programs) {
+  GuPlan p;
+  const int64_t nk = hidden / kGuBK, slabs = inter / kGuSlab, total = nk * slabs;
+  p.programs = std::min(programs, total);
+  for (int64_t s = 0; s < slabs; ++s) {
+    const int64_t parts = gu_owner(s * nk + nk - 1, total, p.programs) - gu_owner(s * nk, total, p.programs) + 1;
+    p.max_parts = std::max(p.max_parts, parts);
+  }
+  return p;
+}
+
+}  // namespace
+}  // namespace ember
+
+using namespace ember;
+
+extern "C" {
+
+int64_t ember_gate_up_silu_workspace_bytes(int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups) {
+  if (tokens < 1 || tokens > kGuMaxTokens || hidden < kGuBK || hidden % kGuBK != 0 || inter < kGuSlab ||
+      inter % kGuSlab != 0 || num_workgroups < 1)
+    return -1;
+  const GuPlan p = gu_plan(hidden, inter, num_workgroups);
+  if (p.programs == 0) return -1;
+  const int64_t slabs = inter / kGuSlab;
+  const int64_t partials = slabs * p.max_parts * gu_partial_floats(tokens) * int64_t(sizeof(float));
+  return partials + (slabs * int64_t(sizeof(uint32_t)) + 255) / 256 * 256;
+}
+
+int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
+                       int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
+                       int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+  if (tokens == 0) return EMBER_OK;
+  if (tokens < 0 || tokens > kGuMaxTokens || hidden < kGuBK || hidden % kGuBK != 0 || inter < kGuSlab ||
+      inter % kGuSlab != 0 || inter > (int64_t(1) << 29) || hidden > (int64_t(1) << 24) || num_workgroups < 1)
+    return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || w == nullptr || out == nullptr || workspace == nullptr || !aligned16(x) || !aligned16(w) ||
+      !aligned16(out) || !aligned16(workspace))
+    return EMBER_EINVAL;
+  // 16-byte rows and 8-byte output packs
+  if (x_row_stride < hidden || w_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 ||
+      w_row_stride % 8 != 0 || out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  const int64_t need = ember_gate_up_silu_workspace_bytes(tokens, hidden, inter, num_workgroups);
+  if (need < 0 || workspace_bytes < need) return EMBER_EINVAL;
+  const GuPlan p = gu_plan(hidden, inter, num_workgroups);
+  GuArgs a{};
+  a.x = x;
+  a.xs = x_row_stride;
+  a.w = w;
+  a.ws = w_row_stride;
+  a.out = out;
+  a.os = out_row_stride;
+  a.T = static_cast<int>(tokens);
+  a.H = static_cast<int>(hidden);
+  a.I = static_cast<int>(inter);
+  a.max_parts = p.max_parts;
+  const int64_t slabs = inter / kGuSlab;
+  a.part = static_cast<float*>(workspace);
+  a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
+                                           slabs * p.max_parts * gu_partial_floats(tokens) * int64_t(sizeof(float)));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == EMBER_F16 ? launch_gu_typed<_Float16>(a, p.programs, st)
+                            : launch_gu_typed<__bf16>(a, p.programs, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+"""The dense MLP's gate_up projection with silu_and_mul as its epilogue, for decode-sized
+batches: `silu_and_mul(gate_up_proj(x))` of Qwen2MLP.forward (emberserve/model/qwen2.py:
+60-61) as one launch of `ember_gate_up_silu` (libember_ops.so).
+
+    x [..., H] (T = prod of leading dims <= 64 tokens), weight [2I, H] (rows [0, I) gate,
+    [I, 2I) up: nn.Linear(H, 2I).weight, qwen2.py:49-57) -> out [..., I]
+
+Numerics: the unfused pair's. The projection's output is rounded to the activation dtype
+before silu_and_mul reads it (ops.py:84-87), so g and u are rounded dot products; the dot
+products are fp32 MFMA sums whose term order is the kernel's own, so results agree with
+another GEMM to within that rounding.
+
+Dispatch: by default the kernel runs for up to FUSED_TOKENS tokens, where it measured
+faster than the unfused pair (torch's linear, i.e. hipBLASLt, then this library's
+silu_and_mul) on MI355X: Qwen3-8B (H 4096, I 12288) 40 vs 45 us at 1-16 tokens, Qwen2.5-7B
+(H 3584, I 18944) 54.5 vs 54.8 us. From 32 tokens on the library GEMM was as fast or faster,
+so the unfused pair runs there; `fused=True` forces the kernel (up to 64 tokens) and
+`fused=False` the pair. Where the kernel does not apply (more than 64 tokens, fp32, shapes
+that are not multiples of 64, unaligned operands) the pair runs. CPU tensors, or
+`EMBERSERVE_FUSED_OPS=0`, take the eager forms.
+
+The kernel is persistent: `num_workgroups` workgroups (default one per CU) take equal runs
+of (64-column slab, 64-k step) units; a slab shared by several runs is merged from
+partials. The count comes from the device only and the partial scratch is cached per
+shape, so a captured HIP graph replays exactly what was captured.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib, ops
+from .ops import _launch, _require_device, fused_enabled
+from .paged_decode import num_sms
+
+MAX_TOKENS = 64    # the kernel's limit
+FUSED_TOKENS = 16  # default dispatch: the kernel up to here, the unfused pair above
+SLAB = 64          # output columns per workgroup
+STEP = 64          # k per pipeline stage
+SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def gate_up_silu_workgroups(device: torch.device) -> int:
+    """Persistent workgroups: one per CU (a workgroup's four waves keep three stages of
+    16 KB weight loads in flight, enough for a CU's share of HBM bandwidth)."""
+    return num_sms(device)
+
+
+class _Scratch:
+    """Partials and arrival counters, zero-filled once and cached per (workgroups, token
+    tile count, hidden, inter, device) so graph replays see captured addresses."""
+
+    def __init__(self) -> None:
+        self._bufs: dict[tuple, Tensor] = {}
+
+    def get(self, programs: int, tokens: int, hidden: int, inter: int, device: torch.device) -> Tensor:
+        key = (programs, -(-tokens // 16), hidden, inter, str(device))
+        buf = self._bufs.get(key)
+        if buf is None:
+            nbytes = _lib.load().ember_gate_up_silu_workspace_bytes(16 * key[1], hidden, inter, programs)
+            if nbytes < 0:
+                raise ValueError(f"gate_up_silu: no plan for hidden {hidden}, inter {inter}, {programs} workgroups")
+            buf = torch.zeros(max(nbytes, 256) // 4, dtype=torch.float32, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_SCRATCH = _Scratch()
+
+
+def gate_up_silu_torch(x: Tensor, weight: Tensor) -> Tensor:
+    """The unfused pair: silu_and_mul(F.linear(x, weight))."""
+    return ops.silu_and_mul(F.linear(x, weight))
+
+
+def _fits(x2: Tensor, weight: Tensor, out: Tensor) -> bool:
+    T, H = x2.shape
+    I = weight.shape[0] // 2
+    return (1 <= T <= MAX_TOKENS and x2.dtype == weight.dtype == out.dtype and x2.dtype in SUPPORTED_DTYPES
+            and H % STEP == 0 and I % SLAB == 0 and I >= SLAB
+            and x2.stride(1) == 1 and weight.stride(1) == 1 and out.stride(1) == 1
+            and x2.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0 and out.stride(0) % 4 == 0
+            and x2.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0)
+
+
+def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None,
+                 fused: bool | None = None) -> Tensor:
+    """silu_and_mul(F.linear(x, weight)) with weight [2I, H] (qwen2.py:60-61)."""
+    if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
+        raise ValueError(f"gate_up_silu: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
+                         "a [2I, H] gate_up projection")
+    if not fused_enabled(x):
+        return gate_up_silu_torch(x, weight)
+    _require_device("gate_up_silu", x, weight)
+    H = x.shape[-1]
+    I = weight.shape[0] // 2
+    x2 = x.reshape(-1, H)
+    T = x2.shape[0]
+    out = torch.empty((T, I), dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out.view(*x.shape[:-1], I)
+    if fused is False or (fused is None and T > FUSED_TOKENS) or not _fits(x2, weight, out):
+        return gate_up_silu_torch(x, weight)
+    programs = gate_up_silu_workgroups(x.device) if num_workgroups is None else int(num_workgroups)
+    if programs < 1:
+        raise ValueError(f"gate_up_silu: num_workgroups must be >= 1, got {programs}")
+    ws = _SCRATCH.get(programs, T, H, I, x.device)
+    _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
+            x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
+            T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+    return out.view(*x.shape[:-1], I)

@@ -49,6 +49,8 @@
  *                             padded copies, attn/paged_flash.py:259-275
  *   ember_scatter_rows2       the output unpack: index_copy_ + slice copies,
  *                             attn/paged_flash.py:267,276-277
+ *   ember_gate_up_silu        silu_and_mul(gate_up_proj(x)) of Qwen2MLP.forward,
+ *                             emberserve/model/qwen2.py:60-61 (decode-sized batches)
  *   ember_mla_decode          mla_decode, emberserve/attn/mla_triton.py:119-182 (kernel
  *                             :49-116; fp32 definition attn/mla_torch.py:33-53)
  *   ember_mla_decode_workspace_bytes  its split-K scratch size (the _SCRATCH buffers,
@@ -325,6 +327,29 @@ int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_str
                      const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
                      int64_t num_splits, void* workspace, int64_t workspace_bytes,
                      void* out, int64_t out_seq_stride, int64_t out_head_stride, void* stream);
+
+/* Bytes of workspace ember_gate_up_silu needs with num_workgroups workgroups, -1 for invalid
+ * arguments: fp32 partials [inter / 64][parts][4 x ceil(tokens / 16) x 2048] (parts = the
+ * most workgroups that share one 64-column slab) and one uint32 arrival counter per slab. */
+int64_t ember_gate_up_silu_workspace_bytes(int64_t tokens, int64_t hidden, int64_t inter,
+                                           int64_t num_workgroups);
+
+/* The dense MLP's gate_up projection with silu_and_mul as its epilogue, for 1..64 tokens:
+ *   g = round(x[t] . w[j]),  u = round(x[t] . w[inter + j]),
+ *   out[t, j] = round(round(g / (1 + exp(-g))) * u),  j < inter,
+ * the composition silu_and_mul(gate_up_proj(x)) of Qwen2MLP.forward
+ * (emberserve/model/qwen2.py:60-61; weight rows [0, inter) gate, [inter, 2 inter) up,
+ * qwen2.py:49-57; silu_and_mul: ops.py:84-87), with fp32 dot products whose term order is
+ * this kernel's own. x [tokens, hidden], w [2 inter, hidden], out [tokens, inter], fp16 or
+ * bf16 (dtype), unit inner stride, 16-byte aligned, row strides in elements (x and w
+ * multiples of 8, out of 4); hidden and inter multiples of 64. num_workgroups persistent
+ * workgroups (at most one per 64-column x 64-k unit; one per CU is the intended size) split
+ * the units evenly. The workspace (ember_gate_up_silu_workspace_bytes, zero-filled once)
+ * holds partials and counters; the counters are left at zero. Other shapes return
+ * EMBER_EINVAL (the caller keeps the unfused pair). */
+int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
+                       int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
+                       int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
 
 #ifdef __cplusplus
 }

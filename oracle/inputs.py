@@ -44,6 +44,14 @@ def silu_inputs(tokens: int, inter: int, dtype, seed: int = 0):
     return normal((tokens, 2 * inter), dtype, seed, std=2.0)
 
 
+def gate_up_inputs(tokens: int, hidden: int, inter: int, dtype, seed: int = 0):
+    """The dense MLP's input: activations N(0, 1) [T, H] and a gate_up weight [2I, H] drawn
+    N(0, 1.5 / sqrt(H)), so the projections are about N(0, 1.5^2) as in a trained layer."""
+    x = normal((tokens, hidden), dtype, seed)
+    w = normal((2 * inter, hidden), dtype, seed + 1, std=1.5 / hidden ** 0.5)
+    return x, w
+
+
 def embedding_inputs(tokens: int, vocab: int, hidden: int, dtype, seed: int = 0):
     """Config 4a: table N(0, 0.02), ids uniform over the vocabulary."""
     w = normal((vocab, hidden), dtype, seed, std=0.02)

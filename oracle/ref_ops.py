@@ -36,6 +36,10 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                MQA paged_decode over the c part; the non-absorbed per-head
                                form with random W_UK / W_UV equals the absorbed one
                                (mla_torch.py:1-17 derivation).
+  gate_up_silu                 per-element float64 dot products (Python sums) rounded to
+                               the dtype, then silu_and_mul, on small inputs; unit-vector
+                               weight rows pick single x columns exactly; zero up rows give
+                               zero; the gate and up halves map to rows [0, I) and [I, 2I).
 No function is left unpinned.
 """
 
@@ -85,6 +89,16 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     """emberserve/model/ops.py:84-87 (silu_and_mul_torch)."""
     inter = x.shape[-1] // 2
     return F.silu(x[..., :inter]) * x[..., inter:]
+
+
+def gate_up_silu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """silu_and_mul(gate_up_proj(x)), Qwen2MLP.forward (emberserve/model/qwen2.py:60-61),
+    weight [2I, H] = nn.Linear(H, 2I).weight (rows [0, I) gate, [I, 2I) up,
+    qwen2.py:49-57). The linear layer's output is in x's dtype (rounded) before
+    silu_and_mul; its dot products are formed in float64 here, so the only rounding before
+    the activation's is the one to the dtype."""
+    gate_up = (x.double() @ weight.double().T).to(x.dtype)
+    return silu_and_mul(gate_up)
 
 
 def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -1,0 +1,184 @@
+"""GPU parity of the fused gate_up projection + silu_and_mul (ember_gate_up_silu) against
+the oracle `gate_up_silu` (float64 dot products rounded to the dtype, then silu_and_mul).
+
+Tolerance. The kernel's dot products are fp32 MFMA sums, the oracle's float64. Products
+of two fp16/bf16 values are exact in fp32, and every path through the kernel's sums has at
+most n = H / 32 + 32 + (partials per slab) roundings, so a projection differs from the exact dot product
+by at most n 2^-24 sum_k |x_k w_k| (first order), before its own rounding to the dtype
+(one more ulp). Near-cancelling sums make that many ulps of a small result, which is why
+the bound is in terms of sum |x w| and not of the result. Per element the allowed output
+error is those projection errors (dg, du) carried through the activation
+(|silu'(g)| |u| dg + |silu(g)| du, |silu'| <= 1.1), two ulp of round(silu(g)) times |u|
+(one for a rounding flip, one for the activation's own exp: the silu_and_mul kernel's bar
+against torch's silu), plus 2 ulp of the output; and at least 98% of the elements must be
+bit-identical to the oracle."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+from emberserve_amd import _lib  # noqa: E402
+from emberserve_amd.gate_up_silu import gate_up_silu, gate_up_silu_torch  # noqa: E402
+from oracle import inputs as gen  # noqa: E402
+from oracle import ref_ops as ref  # noqa: E402
+
+DEV = "cuda"
+MANT = {torch.float16: 10, torch.bfloat16: 7}
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _ulp(v: torch.Tensor, dtype) -> torch.Tensor:
+    a = v.abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(a)) - MANT[dtype])
+
+
+def _check(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, min_exact: float = 0.98,
+           parts: int = 64) -> None:
+    dtype = x.dtype
+    want = ref.gate_up_silu(x, w)
+    exact_gu = x.double() @ w.double().T
+    gu = exact_gu.to(dtype).double()
+    absdot = x.double().abs() @ w.double().abs().T
+    n_round = x.shape[1] / 32 + 32 + parts
+    dgu = _ulp(gu, dtype) + n_round * 2.0 ** -24 * absdot
+    inter = w.shape[0] // 2
+    g, u = gu[:, :inter], gu[:, inter:]
+    dg, du = dgu[:, :inter], dgu[:, inter:]
+    sig = torch.sigmoid(g)
+    dsilu = (sig * (1 + g * (1 - sig))).abs().clamp_max(1.1)
+    act = g * sig
+    tol = (dsilu * u.abs() * dg + act.abs() * du + dg * du + 2 * _ulp(act, dtype) * u.abs()
+           + 2 * _ulp(want.double(), dtype))
+    gotd = got.cpu().double()
+    err = (gotd - want.double()).abs()
+    bad = err > tol
+    if bool(bad.any()):
+        i = int((err / tol).flatten().argmax())
+        t, j = divmod(i, inter)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {err.numel()} out of tolerance, worst ratio "
+                             f"{float((err / tol).max()):.2f} at [{t}, {j}]: g {float(g[t, j])!r} "
+                             f"u {float(u[t, j])!r} got {float(gotd[t, j])!r} want {float(want[t, j])!r}")
+    exact = float((gotd == want.double()).float().mean())
+    assert exact >= min_exact, f"{what}: only {exact:.4f} of the elements bit-exact"
+
+
+@pytest.fixture(autouse=True)
+def _clear_errors():
+    _lib.read_errors(clear=True)
+    yield
+    assert _lib.read_errors() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens", [1, 5, 16, 17, 33, 64])
+def test_gate_up_silu_small_model(dtype, tokens):
+    """Qwen2.5-0.5B MLP (H 896, I 4864): every token-tile count; one workgroup per CU (runs
+    of about 4 units, so most slabs merge partials), 7 workgroups (runs of many whole slabs
+    and a shared one), and one workgroup (everything written directly)."""
+    x, w = gen.gate_up_inputs(tokens, 896, 4864, dtype, seed=tokens)
+    dx, dw = x.to(DEV), w.to(DEV)
+    for programs in (None, 7, 1):
+        _say(f"gate_up_silu 0.5B T={tokens} {dtype} workgroups={programs}")
+        _check(gate_up_silu(dx, dw, num_workgroups=programs, fused=True), x, w, f"T={tokens} workgroups={programs}")
+
+
+@pytest.mark.parametrize("tokens", [1, 32, 64])
+def test_gate_up_silu_qwen3_8b(tokens):
+    """Qwen3-8B MLP (H 4096, I 12288), bf16: one and two workgroups per CU."""
+    x, w = gen.gate_up_inputs(tokens, 4096, 12288, torch.bfloat16, seed=100 + tokens)
+    dx, dw = x.to(DEV), w.to(DEV)
+    for programs in (None, 512):
+        _say(f"gate_up_silu Qwen3-8B T={tokens} workgroups={programs}")
+        _check(gate_up_silu(dx, dw, num_workgroups=programs, fused=True), x, w, f"T={tokens} workgroups={programs}")
+
+
+def test_gate_up_silu_qwen25_7b_strided_rows():
+    """Qwen2.5-7B MLP (H 3584, I 18944), x a row-strided view (rows of a wider buffer)."""
+    xb, w = gen.gate_up_inputs(9, 3584 + 64, 18944, torch.bfloat16, seed=7)
+    w = w[:, :3584].contiguous()
+    x = xb[:, :3584]
+    dx = xb.to(DEV)[:, :3584]
+    assert dx.stride(0) == 3584 + 64
+    _say("gate_up_silu Qwen2.5-7B strided x")
+    _check(gate_up_silu(dx, w.to(DEV), fused=True), x, w, "strided x")
+
+
+def test_gate_up_silu_partition_invariance_and_determinism():
+    """Any workgroup count (runs shorter than, equal to and longer than a slab's 16 k
+    steps, and more workgroups than units) gives results within the tolerance; repeated
+    calls are identical."""
+    x, w = gen.gate_up_inputs(20, 1024, 1024, torch.bfloat16, seed=3)
+    dx, dw = x.to(DEV), w.to(DEV)
+    for programs in (1, 3, 16, 100, 256, 300):
+        outs = [gate_up_silu(dx, dw, num_workgroups=programs, fused=True) for _ in range(3)]
+        assert all(torch.equal(o, outs[0]) for o in outs), f"workgroups={programs} not deterministic"
+        _check(outs[0], x, w, f"workgroups={programs}")
+
+
+def test_gate_up_silu_unfused_fallbacks():
+    """Shapes the kernel does not take run the unfused pair (torch linear + silu_and_mul):
+    more than 64 tokens, a hidden size that is not a multiple of 64, fp32; and by default
+    more than FUSED_TOKENS tokens."""
+    for tokens, hidden, inter, dtype in [(65, 256, 128, torch.bfloat16), (4, 200, 128, torch.bfloat16),
+                                         (4, 256, 100, torch.float16), (4, 256, 128, torch.float32),
+                                         (17, 256, 128, torch.bfloat16)]:
+        x, w = gen.gate_up_inputs(tokens, hidden, inter, dtype, seed=tokens + hidden)
+        got = gate_up_silu(x.to(DEV), w.to(DEV), fused=None if tokens == 17 else True)
+        torch.testing.assert_close(got.cpu(), gate_up_silu_torch(x.to(DEV), w.to(DEV)).cpu(), rtol=0, atol=0)
+
+
+def test_gate_up_silu_bad_workgroups_raise():
+    x, w = gen.gate_up_inputs(4, 512, 128, torch.bfloat16, seed=1)
+    with pytest.raises(ValueError):
+        gate_up_silu(x.to(DEV), w.to(DEV), num_workgroups=0)
+
+
+def test_gate_up_silu_default_dispatch_runs_the_kernel():
+    """Up to FUSED_TOKENS tokens the default path is the kernel: with the unfused pair
+    replaced by a raising stand-in it still returns the right result."""
+    from emberserve_amd import gate_up_silu as gus
+    x, w = gen.gate_up_inputs(16, 1024, 512, torch.bfloat16, seed=9)
+    saved = gus.gate_up_silu_torch
+
+    def boom(*a, **kw):
+        raise AssertionError("unfused pair ran")
+    gus.gate_up_silu_torch = boom
+    try:
+        got = gus.gate_up_silu(x.to(DEV), w.to(DEV))
+    finally:
+        gus.gate_up_silu_torch = saved
+    _check(got, x, w, "default dispatch")
+
+
+def test_gate_up_silu_graph_replay():
+    """A captured call replays to the eager result, with other work between replays (the
+    split counters must be back at zero after every call)."""
+    x, w = gen.gate_up_inputs(12, 2048, 2048, torch.bfloat16, seed=5)
+    dx, dw = x.to(DEV), w.to(DEV)
+    programs = 37  # runs of 27-28 units, shorter than a slab's 32 k steps: slabs merge partials
+    want = gate_up_silu(dx, dw, num_workgroups=programs, fused=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gate_up_silu(dx, dw, num_workgroups=programs, fused=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = gate_up_silu(dx, dw, num_workgroups=programs, fused=True)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
+        assert torch.equal(gate_up_silu(dx, dw, num_workgroups=programs, fused=True), want)

@@ -314,3 +314,54 @@ def test_mixed_rows_plan_and_layout_checks():
         MixedRows([1, 0], "cpu")
     with pytest.raises(ValueError):  # host tensors never reach a kernel
         pack_queries(torch.zeros(7, 2, 4), plan)
+
+
+# ---- gate_up + silu_and_mul (host side) ------------------------------------------------------
+def test_gate_up_silu_cpu_path_is_the_unfused_pair():
+    from emberserve_amd.gate_up_silu import gate_up_silu
+    x, w = gen.gate_up_inputs(6, 128, 96, torch.bfloat16, seed=4)
+    got = gate_up_silu(x, w)
+    assert torch.equal(got, ref.silu_and_mul(torch.nn.functional.linear(x, w)))
+    assert gate_up_silu(x.view(2, 3, 128), w).shape == (2, 3, 96)
+    with pytest.raises(ValueError):
+        gate_up_silu(x, w[:, :64])
+    with pytest.raises(ValueError):
+        gate_up_silu(x, w[:95])
+
+
+def test_gate_up_silu_workspace_plan():
+    """Units are (64-column slab, 64-k step) pairs in slab-major order; workgroup b runs
+    units [floor(b total / G), floor((b + 1) total / G)). The workspace holds, per slab, one
+    partial slot per workgroup whose run meets it (counted here by brute force over the
+    units), plus a counter per slab."""
+    lib = _lib.load()
+
+    def expected(tokens, hidden, inter, programs):
+        nk, slabs = hidden // 64, inter // 64
+        total = nk * slabs
+        G = min(programs, total)
+        owner = []
+        for b in range(G):
+            owner += [b] * ((b + 1) * total // G - b * total // G)
+        parts = max(len(set(owner[s * nk:(s + 1) * nk])) for s in range(slabs))
+        floats = 4 * -(-tokens // 16) * 2 * 64 * 4
+        return slabs * parts * floats * 4 + (slabs * 4 + 255) // 256 * 256
+    for args in [(16, 4096, 12288, 256), (64, 3584, 18944, 256), (1, 896, 4864, 256), (5, 128, 64, 256),
+                 (33, 4096, 12288, 512), (16, 1024, 1024, 7)]:
+        assert lib.ember_gate_up_silu_workspace_bytes(*args) == expected(*args), args
+    assert lib.ember_gate_up_silu_workspace_bytes(65, 4096, 12288, 256) == -1
+    assert lib.ember_gate_up_silu_workspace_bytes(16, 4096, 100, 256) == -1
+    assert lib.ember_gate_up_silu_workspace_bytes(16, 100, 128, 256) == -1
+    assert lib.ember_gate_up_silu_workspace_bytes(16, 4096, 128, 0) == -1
+
+
+def test_gate_up_silu_abi_validation():
+    lib = _lib.load()
+
+    def call(tokens=16, hidden=4096, inter=12288, programs=256, dtype=2):
+        return lib.ember_gate_up_silu(None, hidden, None, hidden, dtype, tokens, hidden, inter, programs, None, 0,
+                                      None, inter, None)
+    assert call(tokens=0) == 0
+    for bad in (dict(tokens=65), dict(hidden=100), dict(inter=100), dict(programs=0), dict(dtype=0)):
+        assert call(**bad) == 1, bad
+    assert call() == 1  # null pointers

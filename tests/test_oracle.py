@@ -235,6 +235,42 @@ def test_silu_special_values():
     torch.testing.assert_close(out[0, 3], torch.tensor(1.0 / (1 + math.exp(-1.0)) * -1.0))
 
 
+# ---------------------------------------------------------------- gate_up + silu_and_mul
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gate_up_silu_brute_force(dtype):
+    """Per element: Python float sums of x[t, k] * w[j, k] rounded to the dtype (the linear
+    layer's output), then the activation in float64 rounded as silu_and_mul rounds."""
+    x, w = gen.gate_up_inputs(3, 24, 5, dtype, seed=11)
+    got = ref.gate_up_silu(x, w)
+    assert got.shape == (3, 5) and got.dtype == dtype
+    xs, ws = x.double().tolist(), w.double().tolist()
+    for t in range(3):
+        for j in range(5):
+            g = torch.tensor(math.fsum(a * b for a, b in zip(xs[t], ws[j])), dtype=torch.float64).to(dtype)
+            u = torch.tensor(math.fsum(a * b for a, b in zip(xs[t], ws[5 + j])), dtype=torch.float64).to(dtype)
+            gd, ud = float(g), float(u)
+            act = torch.tensor(gd / (1 + math.exp(-gd)), dtype=torch.float64).to(dtype)
+            want = torch.tensor(float(act) * ud, dtype=torch.float64).to(dtype)
+            assert_ulp(got[t:t + 1, j:j + 1], want.view(1, 1), 1, f"t={t} j={j}")
+
+
+def test_gate_up_silu_unit_rows_and_halves():
+    """Gate row j = e_(2j), up row j = e_(2j+1) * 2: g and u are single x entries exactly, so
+    out = silu_and_mul of those entries; the halves are rows [0, I) and [I, 2I)."""
+    H, I = 16, 4
+    x = _rand(2, H, dtype=torch.bfloat16, seed=3)
+    w = torch.zeros(2 * I, H, dtype=torch.bfloat16)
+    for j in range(I):
+        w[j, 2 * j] = 1.0
+        w[I + j, 2 * j + 1] = 2.0
+    got = ref.gate_up_silu(x, w)
+    pairs = torch.cat([x[:, 0::2][:, :I], x[:, 1::2][:, :I] * 2], dim=1)
+    assert torch.equal(got, ref.silu_and_mul(pairs))
+    w[I:] = 0
+    assert torch.equal(ref.gate_up_silu(x, w), torch.zeros(2, I, dtype=torch.bfloat16))
+
+
 # ---------------------------------------------------------------- embedding
 
 def test_embedding_matches_numpy_take():
