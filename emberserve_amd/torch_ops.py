@@ -25,7 +25,8 @@ from torch.library import custom_op
 from . import ops as _ops
 
 __all__ = ["rmsnorm", "fused_add_rmsnorm", "rope", "silu_and_mul", "embedding", "qk_norm_rope",
-           "mla_latent_rope", "kv_cache_write", "latent_cache_write", "paged_attention_decode", "mla_decode"]
+           "mla_latent_rope", "kv_cache_write", "latent_cache_write", "paged_attention_decode", "mla_decode",
+           "gate_up_silu"]
 
 
 def _empty(shape, like: Tensor) -> Tensor:
@@ -83,6 +84,19 @@ def _silu_and_mul(x: Tensor) -> Tensor:
 @_silu_and_mul.register_fake
 def _(x):
     return _empty(tuple(x.shape[:-1]) + (x.shape[-1] // 2,), x)
+
+
+# ---- gate_up projection + silu_and_mul (model/qwen2.py:60-61) -----------------------------
+
+@custom_op("emberserve::gate_up_silu", mutates_args=())
+def _gate_up_silu(x: Tensor, weight: Tensor) -> Tensor:
+    from .gate_up_silu import gate_up_silu as impl
+    return impl(x, weight)
+
+
+@_gate_up_silu.register_fake
+def _(x, weight):
+    return _empty(tuple(x.shape[:-1]) + (weight.shape[0] // 2,), x)
 
 
 # ---- embedding (nn.Embedding in model/qwen2.py:172) ---------------------------------------
@@ -196,6 +210,10 @@ def silu_and_mul(x: Tensor) -> Tensor:
 
 def embedding(ids: Tensor, weight: Tensor) -> Tensor:
     return torch.ops.emberserve.embedding(ids, weight)
+
+
+def gate_up_silu(x: Tensor, weight: Tensor) -> Tensor:
+    return torch.ops.emberserve.gate_up_silu(x, weight)
 
 
 def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, eps: float, cos: Tensor,

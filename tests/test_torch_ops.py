@@ -34,6 +34,7 @@ def _cases(device: str):
     latent = gen.normal((5, 192), bf, 7)
     qd, kcd, vcd, bt, cl = gen.decode_inputs([5, 19], 4, 2, 64, 16, torch.float32, seed=8)
     qa, lat, bt2, cl2 = gen.mla_decode_inputs([5, 40], 4, 32, 16, 16, torch.float32, seed=9)
+    gx, gw = gen.gate_up_inputs(3, 128, 64, bf, seed=10)
 
     def dev(*ts):
         return tuple(t.to(d) for t in ts)
@@ -52,6 +53,7 @@ def _cases(device: str):
         ("latent_cache_write", dev(latent, slots, lat_cache)),
         ("paged_attention_decode", dev(qd, kcd, vcd, bt, cl) + (0.125, None)),
         ("mla_decode", dev(qa[..., :32].contiguous(), qa[..., 32:].contiguous(), lat, bt2, cl2) + (0.3, 32, None)),
+        ("gate_up_silu", dev(gx, gw)),
     ]
 
 
