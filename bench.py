@@ -374,6 +374,25 @@ def _ops(torch, ops, tables):
         out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
                       lambda a: gate_up_silu_torch(a[0], a[1]), wbytes))
 
+    def moe_gate_up(cfg, n):
+        """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's
+        geometry (H 2048, I 1408, 64 experts, top-6), decode batch n: bytes are the used
+        experts' weights (each read once) plus x and the activations."""
+        from emberserve_amd.moe import moe_align, moe_gate_up_silu
+        h, inter, ne, k = 2048, 1408, 64, 6
+        g.manual_seed(290 + n)
+        ids = torch.stack([torch.randperm(ne, generator=g, device=dev)[:k] for _ in range(n)])
+        used = int(torch.unique(ids).numel())
+        sorted_ids, block_expert, nv = moe_align(ids, ne)
+
+        def make(i):
+            return (randn((n, h), bf, 300 + i, std=0.5), randn((ne, 2 * inter, h), bf, 310 + i, std=h ** -0.5))
+        wbytes = used * 2 * inter * h * 2
+        nbytes = wbytes + n * h * 2 + n * k * inter * 2
+        out.append(Op("moe_gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts ({used} used), "
+                      f"w[{ne},{2 * inter},{h}] bf16", nbytes, make,
+                      lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k), ne * 2 * inter * h * 2))
+
     add_norm("1", 256, 896, f16)
     rope("2", 256)
     rope("2", 4096)
@@ -418,6 +437,8 @@ def _ops(torch, ops, tables):
     for t in (1, 16):
         gate_up("mlp", t, 4096, 12288, "qwen3-8b")
         gate_up("mlp", t, 3584, 18944, "qwen2.5-7b")
+    for n in (1, 8, 64):
+        moe_gate_up("moe", n)
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
     # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the

@@ -64,6 +64,8 @@ SIGNATURES: dict[str, list] = {
                          _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _p, _i64, _p, _i64, _i64, _p],
     "ember_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],
     "ember_gate_up_silu": [_p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
+    "ember_moe_gate_up_silu": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
+                               _p, _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],

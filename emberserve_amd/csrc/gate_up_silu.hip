@@ -383,6 +383,125 @@ GuPlan gu_plan(int64_t hidden, int64_t inter, int64_t programs) {
   return p;
 }
 
+
+// ---------------------------------------------------------------- routed experts (MoE)
+//
+// The grouped form of the routed experts' gate_up projection + silu_and_mul
+// (fused_moe_forward, emberserve/model/moe_triton.py:332-345: _grouped_gemm over the
+// moe_align layout, then ops.silu_and_mul): for every assignment id = token * k + choice
+// placed in a 16-row block of expert e = block_expert[b],
+//   out[id, j] = round(round(silu(g)) * u),  g = round(x[id / k] . W[e, j]),
+//   u = round(x[id / k] . W[e, I + j]).
+// One workgroup per (block, 64-column slab) over the whole k range; blocks past the last
+// expert (block_expert >= E) exit at once, padding rows (sorted_ids >= num_valid) are
+// computed on row 0 and not stored. The per-step ring, operand layout and epilogue are
+// k_gate_up_silu's with one 16-row token tile and private x copies.
+struct MoeGuArgs {
+  const void* x;
+  int64_t xs, ntok;
+  const void* w;
+  int64_t wes, ws;  // expert and row strides of the [E, 2I, H] weight (elements)
+  void* out;
+  int64_t os;
+  const int32_t* sorted_ids;
+  const int32_t* block_expert;
+  int E, H, I, num_valid, a_div;
+  uint32_t* err;
+};
+
+template <typename T, int NS>
+__global__ void __launch_bounds__(kGuWaves * kWave, 1)
+k_moe_gate_up_silu(MoeGuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  constexpr int XB = 2;   // one 16-row token tile: two 8-row blocks, per wave
+  constexpr int WB = 4;
+  constexpr int WBYTES = kGuWaves * WB * 1024;
+  constexpr int STAGE = WBYTES + kGuWaves * XB * 1024;
+  constexpr int LPS = WB + XB;
+  static_assert(NS >= 2 && NS <= 4, "stages");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NS * STAGE];
+
+  const int blk = blockIdx.x;
+  const int e = a.block_expert[blk];  // uniform (scalar load)
+  if (e < 0 || e >= a.E) return;
+  const int slab = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int nk = a.H / kGuBK;
+  const int lr = lane >> 3;
+  const int lc = (lane & 7) ^ lr;
+
+  const T* xg = static_cast<const T*>(a.x);
+  const T* wg = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes;
+  const T* wsrc[WB];
+#pragma unroll
+  for (int q = 0; q < WB; ++q) {
+    const int row = (q < 2 ? 0 : a.I) + slab * kGuSlab + w * kGuRows + 8 * (q & 1) + lr;
+    wsrc[q] = wg + static_cast<int64_t>(row) * a.ws + 8 * lc;
+  }
+  const T* xsrc[XB];
+#pragma unroll
+  for (int q = 0; q < XB; ++q) {
+    const int id = a.sorted_ids[blk * 16 + 8 * q + lr];
+    int64_t row = id >= 0 && id < a.num_valid ? id / a.a_div : 0;
+    if (row >= a.ntok) {
+      atomicOr(a.err, EMBER_ERR_ROW_INDEX);
+      row = 0;
+    }
+    xsrc[q] = xg + row * a.xs + 8 * lc;
+  }
+  auto issue = [&](int j) {
+    unsigned char* st = lds + (j % NS) * STAGE;
+    const int kk = j * kGuBK;
+#pragma unroll
+    for (int q = 0; q < WB; ++q) gu_load_lds16(wsrc[q] + kk, st + (w * WB + q) * 1024);
+#pragma unroll
+    for (int q = 0; q < XB; ++q) gu_load_lds16(xsrc[q] + kk, st + WBYTES + (w * XB + q) * 1024);
+  };
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  auto compute = [&](int j) {
+    const unsigned char* st = lds + (j % NS) * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = n & 7;
+      const int so = (n >> 3) * 1024 + (8 * r + (((4 * h + g) ^ r) & 7)) * 16;
+      const V8 wgate = *reinterpret_cast<const V8*>(st + (w * WB) * 1024 + so);
+      const V8 wup = *reinterpret_cast<const V8*>(st + (w * WB + 2) * 1024 + so);
+      const V8 xv = *reinterpret_cast<const V8*>(st + WBYTES + w * XB * 1024 + so);
+      acc[0] = M::run(wgate, xv, acc[0]);
+      acc[1] = M::run(wup, xv, acc[1]);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j)
+    if (j < nk) issue(j);
+  for (int j = 0; j < nk; ++j) {
+    const int ahead = min(NS - 2, nk - 1 - j);
+    if (ahead >= 2) wait_vm<2 * LPS>();
+    else if (ahead == 1) wait_vm<LPS>();
+    else wait_vm<0>();
+    asm volatile("" ::: "memory");  // this wave's reads of the buffer it refills are done
+    if (j + NS - 1 < nk) issue(j + NS - 1);
+    compute(j);
+  }
+  // lane (n, g): assignment n of the block, output columns slab * 64 + 16 w + 4g + [0, 4)
+  const int id = a.sorted_ids[blk * 16 + n];
+  if (id >= 0 && id < a.num_valid) {
+    const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
+    Pack<T, 4> o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gf = round_to<T>(acc[0][i]);
+      const float uf = round_to<T>(acc[1][i]);
+      const float act = round_to<T>(gf / (1.0f + expf(-gf)));
+      o.v[i] = from_f32<T>(act * uf);
+    }
+    store_pack<T, 4>(static_cast<T*>(a.out) + static_cast<int64_t>(id) * a.os + col, o);
+  }
+}
 }  // namespace
 }  // namespace ember
 
@@ -437,6 +556,51 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return dtype == EMBER_F16 ? launch_gu_typed<_Float16>(a, p.programs, st)
                             : launch_gu_typed<__bf16>(a, p.programs, st);
+}
+
+int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+                           int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
+                           int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
+                           int64_t num_blocks, int64_t num_valid, int64_t top_k, void* out, int64_t out_row_stride,
+                           void* stream) {
+  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  if (num_blocks < 0 || num_blocks > 0x7fffffffLL || num_valid < 0 || num_valid > 0x7fffffffLL || top_k < 1 ||
+      num_tokens < 1 || num_experts < 1 || num_experts > 0x7fffffffLL || hidden < kGuBK || hidden % kGuBK != 0 ||
+      hidden > (int64_t(1) << 24) || inter < kGuSlab || inter % kGuSlab != 0 || inter > (int64_t(1) << 29))
+    return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || w == nullptr || out == nullptr || sorted_ids == nullptr || block_expert == nullptr ||
+      !aligned16(x) || !aligned16(w) || !aligned16(out))
+    return EMBER_EINVAL;
+  if (x_row_stride < hidden || w_row_stride < hidden || w_expert_stride < 2 * inter * w_row_stride ||
+      out_row_stride < inter || x_row_stride % 8 != 0 || w_row_stride % 8 != 0 || w_expert_stride % 8 != 0 ||
+      out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  MoeGuArgs a{};
+  a.x = x;
+  a.xs = x_row_stride;
+  a.ntok = num_tokens;
+  a.w = w;
+  a.wes = w_expert_stride;
+  a.ws = w_row_stride;
+  a.out = out;
+  a.os = out_row_stride;
+  a.sorted_ids = sorted_ids;
+  a.block_expert = block_expert;
+  a.E = static_cast<int>(num_experts);
+  a.H = static_cast<int>(hidden);
+  a.I = static_cast<int>(inter);
+  a.num_valid = static_cast<int>(num_valid);
+  a.a_div = static_cast<int>(top_k);
+  a.err = device_error_word();
+  const dim3 grid(static_cast<uint32_t>(num_blocks), static_cast<uint32_t>(inter / kGuSlab));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16) {
+    hipLaunchKernelGGL((k_moe_gate_up_silu<_Float16, EMBER_GU_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((k_moe_gate_up_silu<__bf16, EMBER_GU_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
+  }
+  return launch_status();
 }
 
 }  // extern "C"

@@ -1,0 +1,110 @@
+"""The routed experts' gate_up projection with silu_and_mul as its epilogue: the first
+grouped GEMM of fused_moe_forward plus the activation (emberserve/model/moe_triton.py:
+332-345) as one launch of `ember_moe_gate_up_silu` (libember_ops.so), over the reference's
+block-aligned expert layout (`moe_align`, moe_triton.py:215-254).
+
+    x [N, H], topk_ids [N, k] -> moe_align -> (sorted_ids, block_expert, num_valid)
+    moe_gate_up_silu(x, w_gate_up [E, 2I, H], sorted_ids, block_expert, num_valid, k)
+        -> act [N * k, I],  act[t * k + c] = silu_and_mul(x[t] @ w_gate_up[topk_ids[t, c]].T)
+
+with the linear layer's output rounded to the activation dtype before the activation, as
+`_grouped_gemm` stores it. The down projection and the routed-weight sum stay the
+caller's (moe_triton.py:341-345).
+
+CPU tensors, or `EMBERSERVE_FUSED_OPS=0`, take an eager per-block form.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib, ops
+from .ops import _check_indices, _launch, _require_device, fused_enabled
+
+BLOCK_M = 16  # assignments per block (moe_triton.py:38)
+SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tuple[Tensor, Tensor, int]:
+    """The block-aligned expert layout of moe_triton.py:215-254, as device-side torch ops
+    (no host sync). Returns (sorted_ids [max_padded] int32, block_expert [max_blocks]
+    int32, num_valid): assignments id = token * k + choice grouped by expert in ascending
+    id order, each expert's run padded to a multiple of block_m with num_valid, and the
+    expert of every block (num_experts past the last used block)."""
+    n, k = topk_ids.shape
+    num_valid = n * k
+    dev = topk_ids.device
+    flat = topk_ids.reshape(-1).long()
+    max_padded = -(-(num_valid + num_experts * (block_m - 1)) // block_m) * block_m
+    max_blocks = max_padded // block_m
+    order = torch.argsort(flat, stable=True)
+    expert_of = flat[order]
+    counts = torch.zeros(num_experts, dtype=torch.long, device=dev)
+    counts.scatter_add_(0, flat, torch.ones_like(flat))
+    padded = -(-counts // block_m) * block_m
+    pad_start = torch.cumsum(padded, 0) - padded
+    first = torch.cumsum(counts, 0) - counts
+    pos = pad_start[expert_of] + torch.arange(num_valid, device=dev) - first[expert_of]
+    sorted_ids = torch.full((max_padded,), num_valid, dtype=torch.int32, device=dev)
+    sorted_ids[pos] = order.to(torch.int32)
+    block_end = torch.cumsum(padded, 0) // block_m
+    block_expert = torch.searchsorted(block_end, torch.arange(max_blocks, device=dev), right=True).to(torch.int32)
+    return sorted_ids, block_expert, num_valid
+
+
+def moe_gate_up_silu_torch(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor,
+                           num_valid: int, top_k: int) -> Tensor:
+    """Eager form: per used block, silu_and_mul(F.linear(rows, w_gate_up[e])), stored at
+    the blocks' assignment rows."""
+    inter = w_gate_up.shape[1] // 2
+    act = torch.empty((num_valid, inter), dtype=x.dtype, device=x.device)
+    ids = sorted_ids.view(-1, BLOCK_M).tolist()
+    for b, e in enumerate(block_expert.tolist()):
+        if e >= w_gate_up.shape[0]:
+            continue
+        rows = [i for i in ids[b] if i < num_valid]
+        if rows:
+            r = torch.tensor(rows, dtype=torch.long, device=x.device)
+            act[r] = ops.silu_and_mul(F.linear(x[r // top_k], w_gate_up[e]))
+    return act
+
+
+def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
+                     top_k: int) -> Tensor:
+    """act [num_valid, I]: act[id] = silu_and_mul(x[id // top_k] @ w_gate_up[e].T) for every
+    assignment id in a block of expert e (moe_triton.py:339-340, fused)."""
+    assert x.dim() == 2 and w_gate_up.dim() == 3 and w_gate_up.shape[2] == x.shape[1], (x.shape, w_gate_up.shape)
+    assert w_gate_up.shape[1] % 2 == 0
+    assert sorted_ids.dtype == torch.int32 and block_expert.dtype == torch.int32
+    assert sorted_ids.numel() == block_expert.numel() * BLOCK_M, (sorted_ids.shape, block_expert.shape)
+    if not fused_enabled(x):
+        return moe_gate_up_silu_torch(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+    _require_device("moe_gate_up_silu", x, w_gate_up, sorted_ids, block_expert)
+    E, two_i, H = w_gate_up.shape
+    inter = two_i // 2
+    out = torch.empty((num_valid, inter), dtype=x.dtype, device=x.device)
+    if num_valid == 0:
+        return out
+    fits = (x.dtype == w_gate_up.dtype and x.dtype in SUPPORTED_DTYPES and H % 64 == 0 and inter % 64 == 0
+            and x.stride(1) == 1 and w_gate_up.stride(2) == 1 and x.stride(0) % 8 == 0
+            and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and w_gate_up.data_ptr() % 16 == 0
+            and sorted_ids.is_contiguous() and block_expert.is_contiguous())
+    if not fits:
+        return moe_gate_up_silu_torch(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+    _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
+            x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
+            _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
+            block_expert.numel(), num_valid, top_k, out.data_ptr(), out.stride(0))
+    if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
+        raise IndexError("emberserve_amd.moe_gate_up_silu: assignment id past the token rows")
+    return out
+
+
+def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor) -> Tensor:
+    """moe_align + moe_gate_up_silu: the routed experts' activations [N * k, I] in
+    assignment order (the `act` of moe_triton.py:341)."""
+    sorted_ids, block_expert, num_valid = moe_align(topk_ids, w_gate_up.shape[0])
+    return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1])

@@ -51,6 +51,8 @@
  *                             attn/paged_flash.py:267,276-277
  *   ember_gate_up_silu        silu_and_mul(gate_up_proj(x)) of Qwen2MLP.forward,
  *                             emberserve/model/qwen2.py:60-61 (decode-sized batches)
+ *   ember_moe_gate_up_silu    the routed experts' grouped gate_up GEMM + silu_and_mul of
+ *                             fused_moe_forward, emberserve/model/moe_triton.py:332-345
  *   ember_mla_decode          mla_decode, emberserve/attn/mla_triton.py:119-182 (kernel
  *                             :49-116; fp32 definition attn/mla_torch.py:33-53)
  *   ember_mla_decode_workspace_bytes  its split-K scratch size (the _SCRATCH buffers,
@@ -350,6 +352,24 @@ int64_t ember_gate_up_silu_workspace_bytes(int64_t tokens, int64_t hidden, int64
 int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
                        int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
                        int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+
+/* The routed experts' gate_up projection with silu_and_mul as its epilogue, over the
+ * moe_align layout (fused_moe_forward, emberserve/model/moe_triton.py:332-345: the first
+ * _grouped_gemm and ops.silu_and_mul). sorted_ids [num_blocks * 16] int32 holds assignment
+ * ids id = token * top_k + choice (>= num_valid: padding), block_expert [num_blocks] int32
+ * the expert of each 16-row block (>= num_experts: unused block), as moe_align returns them
+ * (moe_triton.py:215-254). For every assignment id in a block of expert e:
+ *   out[id, j] = round(round(silu(g)) * u),  g = round(x[id / top_k] . w[e, j]),
+ *   u = round(x[id / top_k] . w[e, inter + j]),  j < inter.
+ * x [num_tokens, hidden], w [num_experts, 2 inter, hidden] (element strides; unit inner
+ * stride), out [num_valid, inter]; fp16 or bf16, 16-byte aligned, hidden and inter
+ * multiples of 64. A row id / top_k >= num_tokens reads row 0 and sets
+ * EMBER_ERR_ROW_INDEX. */
+int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+                           int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
+                           int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
+                           int64_t num_blocks, int64_t num_valid, int64_t top_k, void* out, int64_t out_row_stride,
+                           void* stream);
 
 #ifdef __cplusplus
 }

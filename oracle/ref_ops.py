@@ -40,6 +40,9 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                the dtype, then silu_and_mul, on small inputs; unit-vector
                                weight rows pick single x columns exactly; zero up rows give
                                zero; the gate and up halves map to rows [0, I) and [I, 2I).
+  moe_gate_up_silu             every token routed to one expert equals gate_up_silu with
+                               that expert's weight, row by row; rows follow the assignment
+                               order t * k + c; experts are picked by index, not position.
 No function is left unpinned.
 """
 
@@ -99,6 +102,19 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     the activation's is the one to the dtype."""
     gate_up = (x.double() @ weight.double().T).to(x.dtype)
     return silu_and_mul(gate_up)
+
+
+def moe_gate_up_silu(x: torch.Tensor, topk_ids: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+    """The routed experts' activations of fused_moe_forward (emberserve/model/moe_triton.py:
+    332-341), defined per assignment as DeepseekMoE.expert computes them (moe.py:117-120):
+    row t * k + c is silu_and_mul(x[t] @ w_gate_up[topk_ids[t, c]].T), the projection
+    rounded to x's dtype (the grouped GEMM's output) before the activation."""
+    n, k = topk_ids.shape
+    rows = []
+    for t in range(n):
+        for c in range(k):
+            rows.append(gate_up_silu(x[t:t + 1], w_gate_up[int(topk_ids[t, c])]))
+    return torch.cat(rows, dim=0)
 
 
 def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -71,3 +71,46 @@ def assert_rope_of_norm_close(got: torch.Tensor, want: torch.Tensor, y_ref: torc
     assert not bool(bad.any()), (
         f"{what}: {int(bad.sum())} of {bad.numel()} elements outside the propagated norm "
         f"tolerance (worst excess {float((diff - bound).max()):.3g})")
+
+
+_MANT = {torch.float16: 10, torch.bfloat16: 7}
+
+
+def _ulp_of(v: torch.Tensor, dtype) -> torch.Tensor:
+    a = v.abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(a)) - _MANT[dtype])
+
+
+def check_gate_up(got: torch.Tensor, want: torch.Tensor, gu: torch.Tensor, absdot: torch.Tensor, hidden: int,
+                  what: str, min_exact: float = 0.98, parts: int = 64) -> None:
+    """A fused gate_up + silu_and_mul result against the oracle. `gu` [rows, 2I] holds the
+    projections rounded to the dtype (float64 dot products), `absdot` the matching sums of
+    |x_k w_k|. The kernel's fp32 sums differ from the exact dot product by at most
+    n 2^-24 sum|x w| (n = hidden / 32 + 32 + parts roundings on any path; products of two
+    fp16/bf16 values are exact in fp32), plus their own rounding to the dtype (one ulp).
+    Those projection errors are carried through the activation; two ulp of round(silu(g))
+    times |u| (a rounding flip, and the activation's own exp against torch's silu) and two
+    ulp of the output are added. At least `min_exact` of the elements must be
+    bit-identical."""
+    dtype = want.dtype
+    gu = gu.double()
+    inter = gu.shape[1] // 2
+    dgu = _ulp_of(gu, dtype) + (hidden / 32 + 32 + parts) * 2.0 ** -24 * absdot.double()
+    g, u = gu[:, :inter], gu[:, inter:]
+    dg, du = dgu[:, :inter], dgu[:, inter:]
+    sig = torch.sigmoid(g)
+    dsilu = (sig * (1 + g * (1 - sig))).abs().clamp_max(1.1)
+    act = g * sig
+    tol = (dsilu * u.abs() * dg + act.abs() * du + dg * du + 2 * _ulp_of(act, dtype) * u.abs()
+           + 2 * _ulp_of(want.double(), dtype))
+    gotd = got.cpu().double()
+    err = (gotd - want.double()).abs()
+    bad = err > tol
+    if bool(bad.any()):
+        i = int((err / tol).flatten().argmax())
+        t, j = divmod(i, inter)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {err.numel()} out of tolerance, worst ratio "
+                             f"{float((err / tol).max()):.2f} at [{t}, {j}]: g {float(g[t, j])!r} "
+                             f"u {float(u[t, j])!r} got {float(gotd[t, j])!r} want {float(want[t, j])!r}")
+    exact = float((gotd == want.double()).float().mean())
+    assert exact >= min_exact, f"{what}: only {exact:.4f} of the elements bit-exact"

@@ -1,17 +1,9 @@
 """GPU parity of the fused gate_up projection + silu_and_mul (ember_gate_up_silu) against
 the oracle `gate_up_silu` (float64 dot products rounded to the dtype, then silu_and_mul).
 
-Tolerance. The kernel's dot products are fp32 MFMA sums, the oracle's float64. Products
-of two fp16/bf16 values are exact in fp32, and every path through the kernel's sums has at
-most n = H / 32 + 32 + (partials per slab) roundings, so a projection differs from the exact dot product
-by at most n 2^-24 sum_k |x_k w_k| (first order), before its own rounding to the dtype
-(one more ulp). Near-cancelling sums make that many ulps of a small result, which is why
-the bound is in terms of sum |x w| and not of the result. Per element the allowed output
-error is those projection errors (dg, du) carried through the activation
-(|silu'(g)| |u| dg + |silu(g)| du, |silu'| <= 1.1), two ulp of round(silu(g)) times |u|
-(one for a rounding flip, one for the activation's own exp: the silu_and_mul kernel's bar
-against torch's silu), plus 2 ulp of the output; and at least 98% of the elements must be
-bit-identical to the oracle."""
+The tolerance is tests.helpers.check_gate_up's: the first-order bound on the fp32
+accumulation error (n 2^-24 sum|x w|) carried through the activation, and at least 98% of
+the elements bit-identical to the oracle."""
 
 from __future__ import annotations
 
@@ -28,9 +20,9 @@ from emberserve_amd import _lib  # noqa: E402
 from emberserve_amd.gate_up_silu import gate_up_silu, gate_up_silu_torch  # noqa: E402
 from oracle import inputs as gen  # noqa: E402
 from oracle import ref_ops as ref  # noqa: E402
+from tests.helpers import check_gate_up  # noqa: E402
 
 DEV = "cuda"
-MANT = {torch.float16: 10, torch.bfloat16: 7}
 
 
 def _say(msg: str) -> None:
@@ -38,39 +30,10 @@ def _say(msg: str) -> None:
     sys.stdout.flush()
 
 
-def _ulp(v: torch.Tensor, dtype) -> torch.Tensor:
-    a = v.abs().clamp_min(2.0 ** -14)
-    return torch.exp2(torch.floor(torch.log2(a)) - MANT[dtype])
-
-
-def _check(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, min_exact: float = 0.98,
-           parts: int = 64) -> None:
-    dtype = x.dtype
-    want = ref.gate_up_silu(x, w)
-    exact_gu = x.double() @ w.double().T
-    gu = exact_gu.to(dtype).double()
+def _check(got: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, min_exact: float = 0.98) -> None:
+    gu = (x.double() @ w.double().T).to(x.dtype)
     absdot = x.double().abs() @ w.double().abs().T
-    n_round = x.shape[1] / 32 + 32 + parts
-    dgu = _ulp(gu, dtype) + n_round * 2.0 ** -24 * absdot
-    inter = w.shape[0] // 2
-    g, u = gu[:, :inter], gu[:, inter:]
-    dg, du = dgu[:, :inter], dgu[:, inter:]
-    sig = torch.sigmoid(g)
-    dsilu = (sig * (1 + g * (1 - sig))).abs().clamp_max(1.1)
-    act = g * sig
-    tol = (dsilu * u.abs() * dg + act.abs() * du + dg * du + 2 * _ulp(act, dtype) * u.abs()
-           + 2 * _ulp(want.double(), dtype))
-    gotd = got.cpu().double()
-    err = (gotd - want.double()).abs()
-    bad = err > tol
-    if bool(bad.any()):
-        i = int((err / tol).flatten().argmax())
-        t, j = divmod(i, inter)
-        raise AssertionError(f"{what}: {int(bad.sum())} of {err.numel()} out of tolerance, worst ratio "
-                             f"{float((err / tol).max()):.2f} at [{t}, {j}]: g {float(g[t, j])!r} "
-                             f"u {float(u[t, j])!r} got {float(gotd[t, j])!r} want {float(want[t, j])!r}")
-    exact = float((gotd == want.double()).float().mean())
-    assert exact >= min_exact, f"{what}: only {exact:.4f} of the elements bit-exact"
+    check_gate_up(got, ref.gate_up_silu(x, w), gu, absdot, x.shape[1], what, min_exact)
 
 
 @pytest.fixture(autouse=True)

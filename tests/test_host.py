@@ -365,3 +365,46 @@ def test_gate_up_silu_abi_validation():
     for bad in (dict(tokens=65), dict(hidden=100), dict(inter=100), dict(programs=0), dict(dtype=0)):
         assert call(**bad) == 1, bad
     assert call() == 1  # null pointers
+
+
+# ---- MoE gate_up + silu_and_mul (host side) -------------------------------------------------
+@pytest.mark.parametrize("n,e,k", [(1, 64, 6), (7, 8, 2), (50, 16, 4), (3, 4, 4)])
+def test_moe_align_layout(n, e, k):
+    """moe_triton.py:215-254's layout: every assignment exactly once, each expert's run in
+    ascending id order starting on a block boundary, padding = num_valid, block_expert the
+    expert of each block (num_experts past the used blocks), sizes as the reference's."""
+    from emberserve_amd.moe import BLOCK_M, moe_align
+    ids = torch.randint(0, e, (n, k), generator=torch.Generator().manual_seed(n * e))
+    sorted_ids, block_expert, nv = moe_align(ids, e)
+    assert nv == n * k
+    max_padded = -(-(nv + e * (BLOCK_M - 1)) // BLOCK_M) * BLOCK_M
+    assert sorted_ids.shape == (max_padded,) and block_expert.shape == (max_padded // BLOCK_M,)
+    s = sorted_ids.tolist()
+    assert sorted(v for v in s if v < nv) == list(range(nv))
+    assert all(v == nv for v in s if v >= nv)
+    flat = ids.reshape(-1).tolist()
+    used_blocks = 0
+    for b, be in enumerate(block_expert.tolist()):
+        blk = [v for v in s[b * BLOCK_M:(b + 1) * BLOCK_M] if v < nv]
+        if be >= e:
+            assert not blk
+            continue
+        used_blocks = b + 1
+        assert all(flat[v] == be for v in blk) and blk == sorted(blk)
+    assert all(be >= e for be in block_expert.tolist()[used_blocks:])
+    assert used_blocks == sum(-(-flat.count(x) // BLOCK_M) for x in range(e))
+
+
+def test_moe_gate_up_cpu_path_follows_the_assignments():
+    """The eager form computes silu_and_mul(F.linear(x[t], w[e])) for row t * k + c with
+    e = topk_ids[t, c], bit for bit against the same ops row by row."""
+    from emberserve_amd.moe import fused_moe_gate_up
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, 64, generator=g).to(torch.bfloat16)
+    w = (torch.randn(6, 2 * 32, 64, generator=g) * 0.2).to(torch.bfloat16)
+    ids = torch.randint(0, 6, (5, 3), generator=g)
+    got = fused_moe_gate_up(x, ids, w)
+    for t in range(5):
+        for c in range(3):
+            want = ref.silu_and_mul(torch.nn.functional.linear(x[t:t + 1], w[int(ids[t, c])]))
+            assert torch.equal(got[t * 3 + c:t * 3 + c + 1], want), (t, c)

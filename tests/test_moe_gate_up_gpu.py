@@ -1,0 +1,76 @@
+"""GPU parity of the routed experts' fused gate_up + silu_and_mul (ember_moe_gate_up_silu)
+over the moe_align layout, against the oracle `moe_gate_up_silu` (per assignment, float64
+dot products rounded to the dtype, then silu_and_mul), at the reference's MoE test geometry
+(tests/test_moe_triton_gpu.py:22-29: Moonlight, H 2048, I 1408, 64 experts, top-6). The
+tolerance is tests.helpers.check_gate_up's."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+if not torch.cuda.is_available():
+    pytest.skip("needs a GPU", allow_module_level=True)
+
+from emberserve_amd import _lib  # noqa: E402
+from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu  # noqa: E402
+from oracle import ref_ops as ref  # noqa: E402
+from tests.helpers import check_gate_up  # noqa: E402
+
+DEV = "cuda"
+H, I, E, K = 2048, 1408, 64, 6
+
+
+def _inputs(n, dtype, seed, experts=E):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(n, H, generator=g) * 0.5).to(dtype)
+    w = (torch.randn(experts, 2 * I, H, generator=g) * 1.5 / H ** 0.5).to(dtype)
+    ids = torch.stack([torch.randperm(experts, generator=g)[:K] for _ in range(n)])
+    return x, w, ids
+
+
+def _check(got, x, w, ids, what):
+    rows = [(t, int(ids[t, c])) for t in range(ids.shape[0]) for c in range(ids.shape[1])]
+    gu = torch.cat([(x[t:t + 1].double() @ w[e].double().T).to(x.dtype) for t, e in rows])
+    absdot = torch.cat([x[t:t + 1].double().abs() @ w[e].double().abs().T for t, e in rows])
+    check_gate_up(got, ref.moe_gate_up_silu(x, ids, w), gu, absdot, H, what, parts=0)
+
+
+@pytest.fixture(autouse=True)
+def _clear_errors():
+    _lib.read_errors(clear=True)
+    yield
+    assert _lib.read_errors() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 8, 37])
+def test_moe_gate_up_matches_oracle(dtype, n):
+    """test_moe_triton_gpu.py:33-43's token counts (200 -> 37 to keep the oracle quick)."""
+    print(f"moe gate_up n={n} {dtype}", flush=True)
+    x, w, ids = _inputs(n, dtype, seed=n)
+    got = fused_moe_gate_up(x.to(DEV), ids.to(DEV), w.to(DEV))
+    assert got.shape == (n * K, I)
+    _check(got, x, w, ids, f"n={n}")
+
+
+def test_moe_gate_up_some_experts_get_no_tokens():
+    """Every token routed to the same six experts: 58 experts idle, one expert's block
+    holds all of a choice's rows (tests/test_moe.py:112-118's case)."""
+    x, w, _ = _inputs(20, torch.bfloat16, seed=5)
+    ids = torch.tensor([[3, 9, 17, 40, 41, 63]] * 20)
+    got = fused_moe_gate_up(x.to(DEV), ids.to(DEV), w.to(DEV))
+    _check(got, x, w, ids, "six experts")
+
+
+def test_moe_gate_up_bad_assignment_sets_error_bit():
+    """An assignment id whose token row is past x reads row 0 and flags EMBER_ERR_ROW_INDEX
+    (every kernel still exits normally)."""
+    x, w, ids = _inputs(4, torch.bfloat16, seed=2)
+    sorted_ids, block_expert, nv = moe_align(ids.to(DEV), E)
+    moe_gate_up_silu(x[:2].to(DEV), w.to(DEV), sorted_ids, block_expert, nv, K)  # rows 2, 3 missing
+    torch.cuda.synchronize()
+    assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX

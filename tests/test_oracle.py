@@ -587,3 +587,16 @@ def test_mixed_unpack_inverts_pack(lens):
     out = torch.full_like(q, float("nan"))
     ref.mixed_unpack(out, q_dec, qpad, lens)
     assert_bitexact(out, q, "unpack(pack(q))")
+
+
+def test_moe_gate_up_silu_oracle_rows_and_experts():
+    """All tokens routed to one expert equal gate_up_silu with that expert's weight; rows
+    follow t * k + c; the expert is picked by index."""
+    x, w0 = gen.gate_up_inputs(4, 32, 8, torch.bfloat16, seed=21)
+    _, w1 = gen.gate_up_inputs(4, 32, 8, torch.bfloat16, seed=22)
+    w = torch.stack([w0, w1])
+    same = ref.moe_gate_up_silu(x, torch.zeros(4, 1, dtype=torch.long), w)
+    assert torch.equal(same, ref.gate_up_silu(x, w0))
+    ids = torch.tensor([[1, 0]] * 4)
+    got = ref.moe_gate_up_silu(x, ids, w)
+    assert torch.equal(got[0::2], ref.gate_up_silu(x, w1)) and torch.equal(got[1::2], ref.gate_up_silu(x, w0))
