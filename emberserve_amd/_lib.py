@@ -65,7 +65,8 @@ SIGNATURES: dict[str, list] = {
     "ember_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],
     "ember_gate_up_silu": [_p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
-                               _p, _i64, _p],
+                               _i64, _p, _i64, _p, _i64, _p],
+    "ember_moe_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],
@@ -73,7 +74,8 @@ SIGNATURES: dict[str, list] = {
 
 _RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspace_bytes": ctypes.c_int64,
             "ember_mla_decode_workspace_bytes": ctypes.c_int64,
-            "ember_gate_up_silu_workspace_bytes": ctypes.c_int64}
+            "ember_gate_up_silu_workspace_bytes": ctypes.c_int64,
+            "ember_moe_gate_up_silu_workspace_bytes": ctypes.c_int64}
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:

@@ -392,10 +392,13 @@ GuPlan gu_plan(int64_t hidden, int64_t inter, int64_t programs) {
 // placed in a 16-row block of expert e = block_expert[b],
 //   out[id, j] = round(round(silu(g)) * u),  g = round(x[id / k] . W[e, j]),
 //   u = round(x[id / k] . W[e, I + j]).
-// One workgroup per (block, 64-column slab) over the whole k range; blocks past the last
-// expert (block_expert >= E) exit at once, padding rows (sorted_ids >= num_valid) are
-// computed on row 0 and not stored. The per-step ring, operand layout and epilogue are
-// k_gate_up_silu's with one 16-row token tile and private x copies.
+// One workgroup per (block, 64-column slab, k split); blocks past the last expert
+// (block_expert >= E) exit at once, padding rows (sorted_ids >= num_valid) are computed on
+// row 0 and not stored. The per-step ring, operand layout and epilogue are
+// k_gate_up_silu's with one 16-row token tile and private x copies. With several k splits
+// (small batches, where blocks x slabs alone leave CUs idle) each split stores fp32
+// partials at its rows' assignment ids, and the last split of a (block, slab) to arrive
+// sums them in k order.
 struct MoeGuArgs {
   const void* x;
   int64_t xs, ntok;
@@ -406,6 +409,9 @@ struct MoeGuArgs {
   const int32_t* sorted_ids;
   const int32_t* block_expert;
   int E, H, I, num_valid, a_div;
+  int kc;             // k per split (gridDim.z splits)
+  float* part;        // [splits][num_valid][2I] fp32 partials (splits > 1)
+  uint32_t* counters; // [num_blocks][I / 64] arrival counters (splits > 1)
   uint32_t* err;
 };
 
@@ -430,12 +436,13 @@ k_moe_gate_up_silu(MoeGuArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  const int nk = a.H / kGuBK;
+  const int nk = a.kc / kGuBK;
+  const int k0 = blockIdx.z * a.kc;
   const int lr = lane >> 3;
   const int lc = (lane & 7) ^ lr;
 
-  const T* xg = static_cast<const T*>(a.x);
-  const T* wg = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes;
+  const T* xg = static_cast<const T*>(a.x) + k0;
+  const T* wg = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes + k0;
   const T* wsrc[WB];
 #pragma unroll
   for (int q = 0; q < WB; ++q) {
@@ -489,8 +496,47 @@ k_moe_gate_up_silu(MoeGuArgs a) {
   }
   // lane (n, g): assignment n of the block, output columns slab * 64 + 16 w + 4g + [0, 4)
   const int id = a.sorted_ids[blk * 16 + n];
-  if (id >= 0 && id < a.num_valid) {
-    const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
+  const bool mine = id >= 0 && id < a.num_valid;
+  const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
+  const int splits = gridDim.z;
+  if (splits > 1) {
+    const int64_t row_floats = 2 * static_cast<int64_t>(a.I);
+    const int part_floats = static_cast<int>(splits * a.num_valid * row_floats);
+    const CoherentRsrc rs = coherent_rsrc(a.part, part_floats);
+    const int off = static_cast<int>(((blockIdx.z * static_cast<int64_t>(a.num_valid) + (mine ? id : 0)) * row_floats + col) * 4);
+    if (mine) {
+      store_coherent<4>(rs, off, acc[0]);
+      store_coherent<4>(rs, off + a.I * 4, acc[1]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int is_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t* cnt = a.counters + static_cast<int64_t>(blk) * gridDim.y + slab;
+      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = prev == static_cast<uint32_t>(splits - 1);
+      if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last || !mine) return;
+    // the splits in k order, all loads in flight together (at most 4 splits)
+    f32x4 v[4][2];
+    const int row0 = static_cast<int>((static_cast<int64_t>(id) * row_floats + col) * 4);
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      const int o = static_cast<int>(min(sp, splits - 1) * static_cast<int64_t>(a.num_valid) * row_floats * 4) + row0;
+      v[sp][0] = load_coherent<4>(rs, o);
+      v[sp][1] = load_coherent<4>(rs, o + a.I * 4);
+    }
+    acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < splits) {
+        acc[0] += v[sp][0];
+        acc[1] += v[sp][1];
+      }
+  }
+  if (mine) {
     Pack<T, 4> o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -502,6 +548,7 @@ k_moe_gate_up_silu(MoeGuArgs a) {
     store_pack<T, 4>(static_cast<T*>(a.out) + static_cast<int64_t>(id) * a.os + col, o);
   }
 }
+
 }  // namespace
 }  // namespace ember
 
@@ -558,12 +605,25 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
                             : launch_gu_typed<__bf16>(a, p.programs, st);
 }
 
+int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter, int64_t num_blocks,
+                                               int64_t num_splits) {
+  if (num_valid < 0 || inter < kGuSlab || inter % kGuSlab != 0 || num_blocks < 0 || num_splits < 1 ||
+      num_splits > 4)
+    return -1;
+  if (num_splits == 1) return 0;
+  const int64_t part = num_splits * num_valid * 2 * inter * int64_t(sizeof(float));
+  if (part >= (int64_t(1) << 31)) return -1;  // one buffer resource addresses the partials
+  return (part + 255) / 256 * 256 + (num_blocks * (inter / kGuSlab) * int64_t(sizeof(uint32_t)) + 255) / 256 * 256;
+}
+
 int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
                            int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
                            int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
-                           int64_t num_blocks, int64_t num_valid, int64_t top_k, void* out, int64_t out_row_stride,
-                           void* stream) {
+                           int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
+                           int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
   if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  if (num_splits < 1 || num_splits > 4 || (hidden / kGuBK) % num_splits != 0 || hidden / kGuBK / num_splits < 2)
+    return EMBER_EINVAL;
   if (num_blocks < 0 || num_blocks > 0x7fffffffLL || num_valid < 0 || num_valid > 0x7fffffffLL || top_k < 1 ||
       num_tokens < 1 || num_experts < 1 || num_experts > 0x7fffffffLL || hidden < kGuBK || hidden % kGuBK != 0 ||
       hidden > (int64_t(1) << 24) || inter < kGuSlab || inter % kGuSlab != 0 || inter > (int64_t(1) << 29))
@@ -592,8 +652,17 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
   a.I = static_cast<int>(inter);
   a.num_valid = static_cast<int>(num_valid);
   a.a_div = static_cast<int>(top_k);
+  a.kc = static_cast<int>(hidden / num_splits);
+  if (num_splits > 1) {
+    const int64_t need = ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, num_splits);
+    if (need < 0 || workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) return EMBER_EINVAL;
+    const int64_t part = num_splits * num_valid * 2 * inter * int64_t(sizeof(float));
+    a.part = static_cast<float*>(workspace);
+    a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + (part + 255) / 256 * 256);
+  }
   a.err = device_error_word();
-  const dim3 grid(static_cast<uint32_t>(num_blocks), static_cast<uint32_t>(inter / kGuSlab));
+  const dim3 grid(static_cast<uint32_t>(num_blocks), static_cast<uint32_t>(inter / kGuSlab),
+                  static_cast<uint32_t>(num_splits));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16) {
     hipLaunchKernelGGL((k_moe_gate_up_silu<_Float16, EMBER_GU_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);

@@ -22,6 +22,7 @@ from torch import Tensor
 
 from . import _lib, ops
 from .ops import _check_indices, _launch, _require_device, fused_enabled
+from .paged_decode import num_sms
 
 BLOCK_M = 16  # assignments per block (moe_triton.py:38)
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
@@ -54,6 +55,41 @@ def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tup
     return sorted_ids, block_expert, num_valid
 
 
+def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, device: torch.device) -> int:
+    """k splits from shapes only: the smallest of 1, 2, 4 that gives at least two
+    workgroups per CU for the blocks that can hold assignments (at most min(num_valid,
+    num_experts) experts are used) over the 64-column slabs, with >= 2 k steps per split.
+    Measured at Moonlight's geometry: one token (6 experts, 132 workgroups unsplit)."""
+    steps = hidden // 64
+    busy = min(num_valid, num_experts) * max(1, inter // 64)
+    for d in (1, 2, 4):
+        if steps % d == 0 and steps // d >= 2 and (busy * d >= 2 * num_sms(device) or d == 4):
+            return d
+    return 1
+
+
+class _Scratch:
+    """Split partials and counters, zero-filled once per (splits, num_valid, inter,
+    num_blocks, device), so graph replays see captured addresses."""
+
+    def __init__(self) -> None:
+        self._bufs: dict[tuple, Tensor] = {}
+
+    def get(self, splits: int, num_valid: int, inter: int, num_blocks: int, device: torch.device) -> Tensor:
+        key = (splits, num_valid, inter, num_blocks, str(device))
+        buf = self._bufs.get(key)
+        if buf is None:
+            nbytes = _lib.load().ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, splits)
+            if nbytes < 0:
+                raise ValueError(f"moe_gate_up_silu: no workspace for {splits} splits, {num_valid} rows")
+            buf = torch.zeros(max(nbytes, 256) // 4, dtype=torch.float32, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_SCRATCH = _Scratch()
+
+
 def moe_gate_up_silu_torch(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor,
                            num_valid: int, top_k: int) -> Tensor:
     """Eager form: per used block, silu_and_mul(F.linear(rows, w_gate_up[e])), stored at
@@ -72,7 +108,7 @@ def moe_gate_up_silu_torch(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, blo
 
 
 def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
-                     top_k: int) -> Tensor:
+                     top_k: int, *, num_splits: int | None = None) -> Tensor:
     """act [num_valid, I]: act[id] = silu_and_mul(x[id // top_k] @ w_gate_up[e].T) for every
     assignment id in a block of expert e (moe_triton.py:339-340, fused)."""
     assert x.dim() == 2 and w_gate_up.dim() == 3 and w_gate_up.shape[2] == x.shape[1], (x.shape, w_gate_up.shape)
@@ -94,17 +130,26 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
             and sorted_ids.is_contiguous() and block_expert.is_contiguous())
     if not fits:
         return moe_gate_up_silu_torch(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+    if num_splits is None:
+        num_splits = moe_num_splits(num_valid, E, H, inter, x.device)
+    num_splits = int(num_splits)
+    if num_splits not in (1, 2, 4) or (H // 64) % num_splits or H // 64 // num_splits < 2:
+        raise ValueError(f"moe_gate_up_silu: num_splits {num_splits} must be 1, 2 or 4 and divide hidden / 64 "
+                         f"= {H // 64} with >= 2 steps per split")
+    ws = _SCRATCH.get(num_splits, num_valid, inter, block_expert.numel(), x.device) if num_splits > 1 else None
     _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
             x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
             _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
-            block_expert.numel(), num_valid, top_k, out.data_ptr(), out.stride(0))
+            block_expert.numel(), num_valid, top_k, num_splits, ws.data_ptr() if ws is not None else None,
+            ws.numel() * 4 if ws is not None else 0, out.data_ptr(), out.stride(0))
     if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
         raise IndexError("emberserve_amd.moe_gate_up_silu: assignment id past the token rows")
     return out
 
 
-def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor) -> Tensor:
+def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None) -> Tensor:
     """moe_align + moe_gate_up_silu: the routed experts' activations [N * k, I] in
     assignment order (the `act` of moe_triton.py:341)."""
     sorted_ids, block_expert, num_valid = moe_align(topk_ids, w_gate_up.shape[0])
-    return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1])
+    return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1],
+                            num_splits=num_splits)

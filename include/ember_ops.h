@@ -364,12 +364,20 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
  * x [num_tokens, hidden], w [num_experts, 2 inter, hidden] (element strides; unit inner
  * stride), out [num_valid, inter]; fp16 or bf16, 16-byte aligned, hidden and inter
  * multiples of 64. A row id / top_k >= num_tokens reads row 0 and sets
- * EMBER_ERR_ROW_INDEX. */
+ * EMBER_ERR_ROW_INDEX. num_splits (1..4, dividing hidden / 64 with >= 2 steps per split)
+ * splits k across workgroups for small batches; with more than one it needs a zero-filled
+ * workspace of ember_moe_gate_up_silu_workspace_bytes, whose counters it leaves at zero. */
 int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
                            int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
                            int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
-                           int64_t num_blocks, int64_t num_valid, int64_t top_k, void* out, int64_t out_row_stride,
-                           void* stream);
+                           int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
+                           int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+
+/* Bytes of workspace ember_moe_gate_up_silu needs for num_splits > 1 (0 for one split), -1
+ * for invalid arguments: fp32 partials [num_splits][num_valid][2 inter] and one uint32
+ * arrival counter per (block, 64-column slab). */
+int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter, int64_t num_blocks,
+                                               int64_t num_splits);
 
 #ifdef __cplusplus
 }

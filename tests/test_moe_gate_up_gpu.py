@@ -52,9 +52,11 @@ def test_moe_gate_up_matches_oracle(dtype, n):
     """test_moe_triton_gpu.py:33-43's token counts (200 -> 37 to keep the oracle quick)."""
     print(f"moe gate_up n={n} {dtype}", flush=True)
     x, w, ids = _inputs(n, dtype, seed=n)
-    got = fused_moe_gate_up(x.to(DEV), ids.to(DEV), w.to(DEV))
-    assert got.shape == (n * K, I)
-    _check(got, x, w, ids, f"n={n}")
+    dx, dids, dw = x.to(DEV), ids.to(DEV), w.to(DEV)
+    for splits in (None, 1, 2, 4):
+        got = fused_moe_gate_up(dx, dids, dw, num_splits=splits)
+        assert got.shape == (n * K, I)
+        _check(got, x, w, ids, f"n={n} splits={splits}")
 
 
 def test_moe_gate_up_some_experts_get_no_tokens():
@@ -64,6 +66,29 @@ def test_moe_gate_up_some_experts_get_no_tokens():
     ids = torch.tensor([[3, 9, 17, 40, 41, 63]] * 20)
     got = fused_moe_gate_up(x.to(DEV), ids.to(DEV), w.to(DEV))
     _check(got, x, w, ids, "six experts")
+
+
+def test_moe_gate_up_split_graph_replay():
+    """Split partials and counters across captured replays, with other work in between:
+    every replay matches the eager result (the counters return to zero)."""
+    x, w, ids = _inputs(2, torch.bfloat16, seed=8)
+    dx, dids, dw = x.to(DEV), ids.to(DEV), w.to(DEV)
+    sorted_ids, block_expert, nv = moe_align(dids, E)
+    want = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=4)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=4)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        got = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=4)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i}"
+        assert torch.equal(moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=4), want)
 
 
 def test_moe_gate_up_bad_assignment_sets_error_bit():
