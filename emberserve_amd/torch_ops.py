@@ -26,7 +26,7 @@ from . import ops as _ops
 
 __all__ = ["rmsnorm", "fused_add_rmsnorm", "rope", "silu_and_mul", "embedding", "qk_norm_rope",
            "mla_latent_rope", "kv_cache_write", "latent_cache_write", "paged_attention_decode", "mla_decode",
-           "gate_up_silu"]
+           "gate_up_silu", "moe_gate_up_silu"]
 
 
 def _empty(shape, like: Tensor) -> Tensor:
@@ -97,6 +97,18 @@ def _gate_up_silu(x: Tensor, weight: Tensor) -> Tensor:
 @_gate_up_silu.register_fake
 def _(x, weight):
     return _empty(tuple(x.shape[:-1]) + (weight.shape[0] // 2,), x)
+
+
+@custom_op("emberserve::moe_gate_up_silu", mutates_args=())
+def _moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
+                      top_k: int) -> Tensor:
+    from .moe import moe_gate_up_silu as impl
+    return impl(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+
+
+@_moe_gate_up_silu.register_fake
+def _(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k):
+    return _empty((num_valid, w_gate_up.shape[1] // 2), x)
 
 
 # ---- embedding (nn.Embedding in model/qwen2.py:172) ---------------------------------------
@@ -214,6 +226,11 @@ def embedding(ids: Tensor, weight: Tensor) -> Tensor:
 
 def gate_up_silu(x: Tensor, weight: Tensor) -> Tensor:
     return torch.ops.emberserve.gate_up_silu(x, weight)
+
+
+def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
+                     top_k: int) -> Tensor:
+    return torch.ops.emberserve.moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
 
 
 def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, eps: float, cos: Tensor,

@@ -35,6 +35,10 @@ def _cases(device: str):
     qd, kcd, vcd, bt, cl = gen.decode_inputs([5, 19], 4, 2, 64, 16, torch.float32, seed=8)
     qa, lat, bt2, cl2 = gen.mla_decode_inputs([5, 40], 4, 32, 16, 16, torch.float32, seed=9)
     gx, gw = gen.gate_up_inputs(3, 128, 64, bf, seed=10)
+    from emberserve_amd.moe import moe_align
+    mw = torch.stack([gen.gate_up_inputs(1, 128, 64, bf, seed=11 + e)[1] for e in range(4)])
+    mids = torch.tensor([[0, 2], [3, 2], [1, 0]])
+    sid, bex, nv = moe_align(mids, 4)
 
     def dev(*ts):
         return tuple(t.to(d) for t in ts)
@@ -54,6 +58,7 @@ def _cases(device: str):
         ("paged_attention_decode", dev(qd, kcd, vcd, bt, cl) + (0.125, None)),
         ("mla_decode", dev(qa[..., :32].contiguous(), qa[..., 32:].contiguous(), lat, bt2, cl2) + (0.3, 32, None)),
         ("gate_up_silu", dev(gx, gw)),
+        ("moe_gate_up_silu", dev(gx, mw, sid, bex) + (nv, 2)),
     ]
 
 
