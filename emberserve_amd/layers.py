@@ -40,6 +40,24 @@ class Embedding(nn.Embedding):
         return super().forward(ids)
 
 
+class SwiGLUMLP(nn.Module):
+    """Qwen2MLP (emberserve/model/qwen2.py:48-61) with the same parameters (`gate_up_proj`
+    [2I, H] with gate rows first, `down_proj` [H, I], no biases), so checkpoints load
+    unchanged; the forward runs gate_up_silu (the fused kernel at decode batches, the
+    unfused pair otherwise). The tensor-parallel all-reduce after down_proj stays the
+    caller's, as in the reference's `tpdist.all_reduce(...)`."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int) -> None:
+        super().__init__()
+        self.intermediate_size = intermediate_size
+        self.gate_up_proj = nn.Linear(hidden_size, 2 * intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from .gate_up_silu import gate_up_silu
+        return self.down_proj(gate_up_silu(x, self.gate_up_proj.weight))
+
+
 def qwen3_pre_attention_rope(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
                              q_norm: RMSNorm, k_norm: RMSNorm, rotary_emb: RotaryEmbedding,
                              positions: torch.Tensor):

@@ -145,3 +145,16 @@ def test_gate_up_silu_graph_replay():
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"replay {i}"
         assert torch.equal(gate_up_silu(dx, dw, num_workgroups=programs, fused=True), want)
+
+
+def test_swiglu_mlp_module_on_the_gpu():
+    """layers.SwiGLUMLP on a decode batch runs the fused kernel: its output equals
+    down_proj of gate_up_silu's result."""
+    from emberserve_amd import layers
+    torch.manual_seed(0)
+    mlp = layers.SwiGLUMLP(1024, 512).to(DEV, torch.bfloat16)
+    x = torch.randn(8, 1024, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        got = mlp(x)
+        want = mlp.down_proj(gate_up_silu(x, mlp.gate_up_proj.weight))
+    assert torch.equal(got, want)

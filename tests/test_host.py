@@ -422,3 +422,13 @@ def test_moe_split_rule_and_workspace(monkeypatch):
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 4) == (4 * 6 * 2816 * 4 + 255) // 256 * 256 + (61 * 22 * 4 + 255) // 256 * 256
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 5) == -1
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 100, 61, 2) == -1
+
+
+def test_swiglu_mlp_module_matches_the_reference_composition():
+    """layers.SwiGLUMLP has Qwen2MLP's parameters and computes down(silu_and_mul(gate_up(x)))."""
+    mlp = layers.SwiGLUMLP(64, 96).to(torch.bfloat16)
+    assert mlp.gate_up_proj.weight.shape == (192, 64) and mlp.down_proj.weight.shape == (64, 96)
+    x = torch.randn(5, 64, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    with torch.no_grad():
+        want = mlp.down_proj(ref.silu_and_mul(mlp.gate_up_proj(x)))
+        assert torch.equal(mlp(x), want)
