@@ -56,15 +56,15 @@ def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tup
 
 
 def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, device: torch.device) -> int:
-    """k splits from shapes only: the smallest of 1, 2, 4 that gives at least two
-    workgroups per CU for the blocks that can hold assignments (at most min(num_valid,
-    num_experts) experts are used) over the 64-column slabs, with >= 2 k steps per split.
-    Measured at Moonlight's geometry: one token (6 experts, 132 workgroups unsplit)."""
+    """k splits from shapes only: 2 while the workgroups of the blocks that can hold
+    assignments (at most min(num_valid, num_experts) experts are used) over the 64-column
+    slabs number under 1.5x the CUs, else 1 (>= 2 k steps per split). Measured at
+    Moonlight's geometry (µs, 1 / 2 / 4 splits): one token 17.5 / 15.9 / 16.8, two 31.5 /
+    25.5 / 30.0, three 40.1 / 44.4 / 46.6, four 48.7 / 54.3 / 55.0."""
     steps = hidden // 64
     busy = min(num_valid, num_experts) * max(1, inter // 64)
-    for d in (1, 2, 4):
-        if steps % d == 0 and steps // d >= 2 and (busy * d >= 2 * num_sms(device) or d == 4):
-            return d
+    if steps % 2 == 0 and steps // 2 >= 2 and busy < 1.5 * num_sms(device):
+        return 2
     return 1
 
 

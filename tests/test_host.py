@@ -414,9 +414,10 @@ def test_moe_split_rule_and_workspace(monkeypatch):
     from emberserve_amd import moe
     monkeypatch.setattr(moe, "num_sms", lambda device: 256)
     dev = torch.device("cpu")
-    assert moe.moe_num_splits(6, 64, 2048, 1408, dev) == 4     # one token: 6 x 22 slabs
-    assert moe.moe_num_splits(48, 64, 2048, 1408, dev) == 1    # eight tokens: 48 x 22 >= 512
-    assert moe.moe_num_splits(12, 64, 2048, 1408, dev) == 2    # two tokens: 264 -> 528
+    assert moe.moe_num_splits(6, 64, 2048, 1408, dev) == 2     # one token: 6 x 22 slabs = 132
+    assert moe.moe_num_splits(12, 64, 2048, 1408, dev) == 2    # two tokens: 264 < 384
+    assert moe.moe_num_splits(18, 64, 2048, 1408, dev) == 1    # three tokens: 396
+    assert moe.moe_num_splits(48, 64, 2048, 1408, dev) == 1    # eight tokens
     lib = _lib.load()
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 1) == 0
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 4) == (4 * 6 * 2816 * 4 + 255) // 256 * 256 + (61 * 22 * 4 + 255) // 256 * 256
