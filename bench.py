@@ -756,7 +756,8 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only; every op is row-independent and shards "
-              "over tokens with no exchange (see DESIGN.md), so --gpus must be 1.", file=sys.stderr)
+              "over tokens (or heads) with no exchange, so one GPU's share is the single-GPU kernel "
+              "at a smaller shape: --gpus must be 1.", file=sys.stderr)
         return 2
 
     import torch
