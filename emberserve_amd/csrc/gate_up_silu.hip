@@ -39,9 +39,11 @@
 #ifndef EMBER_GU_STAGES
 #define EMBER_GU_STAGES 3
 #endif
-// token tiles (of 16) up to which every wave loads its own copy of x
+// Token tiles (of 16) up to which every wave loads its own copy of x. Measured on MI355X
+// (persistent grid, one workgroup per CU): private and shared copies tie at 1-16 tokens;
+// at 32 tokens the shared copy is faster (Qwen3-8B 41.2 vs 41.9 us, Qwen2.5-7B 59.2 vs 61.4).
 #ifndef EMBER_GU_PRIVX_MT
-#define EMBER_GU_PRIVX_MT 2
+#define EMBER_GU_PRIVX_MT 1
 #endif
 
 namespace ember {
