@@ -3,7 +3,9 @@ configurations the main parity file mirrors: the hidden sizes, MLP widths and he
 of the Qwen2.5 / Qwen3 range (0.5B to 72B) and DeepSeek-V2/V3. Each shape takes the kernel
 configuration its size selects (row-team widths, packs per lane, query-head passes), so
 this sweeps those paths against the oracle with the tolerances of tests/test_parity_gpu.py
-(bit-exact residual, rope and embedding; <= 2 ulp for the normalised and silu outputs)."""
+(bit-exact residual, rope and embedding; <= 2 ulp for the normalised and silu outputs).
+The fused gate_up + silu_and_mul rows (Qwen3-4B, Qwen2.5-14B MLPs; DeepSeek-V3's expert
+shape) use tests.helpers.check_gate_up's accumulation-error bound."""
 
 from __future__ import annotations
 
@@ -113,3 +115,38 @@ def test_mla_latent_rope_deepseek_heads(heads):
     assert_bitexact(qd[..., :128], q[..., :128], "q_nope untouched")
     assert_bitexact(got_latent[:, 512:], want_latent[:, 512:], "k_pe")
     assert_ulp(got_latent[:, :512], want_latent[:, :512], 2, "latent c")
+
+
+@pytest.mark.parametrize("hidden,inter", [(2560, 9728), (5120, 13824)])   # Qwen3-4B, Qwen2.5-14B
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_gate_up_silu_model_mlps(hidden, inter, tokens):
+    """The fused gate_up + silu_and_mul at other models' MLP shapes, decode batches."""
+    from emberserve_amd.gate_up_silu import gate_up_silu
+    from tests.helpers import check_gate_up
+    _say(f"gate_up_silu H={hidden} I={inter} T={tokens}")
+    x, w = gen.gate_up_inputs(tokens, hidden, inter, BF, seed=hidden + tokens)
+    got = gate_up_silu(x.to(DEV), w.to(DEV), fused=True)
+    gu = (x.double() @ w.double().T).to(BF)
+    absdot = x.double().abs() @ w.double().abs().T
+    check_gate_up(got, ref.gate_up_silu(x, w), gu, absdot, hidden, f"H={hidden} T={tokens}")
+
+
+def test_moe_gate_up_deepseek_v3_expert_shape():
+    """DeepSeek-V3's routed-expert geometry (H 7168, I 2048, top-8), over 8 experts so the
+    weights stay at 470 MB: every token uses every expert; 1 and 2 k splits."""
+    from emberserve_amd.moe import fused_moe_gate_up
+    from tests.helpers import check_gate_up
+    h, inter, ne, k, n = 7168, 2048, 8, 8, 3
+    g = torch.Generator().manual_seed(77)
+    x = (torch.randn(n, h, generator=g) * 0.5).to(BF)
+    w = (torch.randn(ne, 2 * inter, h, generator=g) * 1.5 / h ** 0.5).to(BF)
+    ids = torch.stack([torch.randperm(ne, generator=g) for _ in range(n)])
+    rows = [(t, int(ids[t, c])) for t in range(n) for c in range(k)]
+    want = ref.moe_gate_up_silu(x, ids, w)
+    gu = torch.cat([(x[t:t + 1].double() @ w[e].double().T).to(BF) for t, e in rows])
+    absdot = torch.cat([x[t:t + 1].double().abs() @ w[e].double().abs().T for t, e in rows])
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    for splits in (1, 2):
+        _say(f"moe gate_up DeepSeek-V3 shape splits={splits}")
+        got = fused_moe_gate_up(dx, dids, dw, num_splits=splits)
+        check_gate_up(got, want, gu, absdot, h, f"V3 splits={splits}", parts=0)
