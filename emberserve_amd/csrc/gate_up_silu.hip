@@ -42,6 +42,12 @@
 // Token tiles (of 16) up to which every wave loads its own copy of x. Measured on MI355X
 // (persistent grid, one workgroup per CU): private and shared copies tie at 1-16 tokens;
 // at 32 tokens the shared copy is faster (Qwen3-8B 41.2 vs 41.9 us, Qwen2.5-7B 59.2 vs 61.4).
+// Ring stages of the routed-expert kernel (one workgroup per block and slab, not persistent).
+// Measured at Moonlight's geometry: 2 stages (48 KB of LDS, three workgroups per CU) are
+// 5-10% slower than 3 at 1-64 tokens (8 tokens: 98.8 vs 89.6 us).
+#ifndef EMBER_MOE_STAGES
+#define EMBER_MOE_STAGES 3
+#endif
 #ifndef EMBER_GU_PRIVX_MT
 #define EMBER_GU_PRIVX_MT 1
 #endif
@@ -667,9 +673,9 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
                   static_cast<uint32_t>(num_splits));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16) {
-    hipLaunchKernelGGL((k_moe_gate_up_silu<_Float16, EMBER_GU_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
+    hipLaunchKernelGGL((k_moe_gate_up_silu<_Float16, EMBER_MOE_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
   } else {
-    hipLaunchKernelGGL((k_moe_gate_up_silu<__bf16, EMBER_GU_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
+    hipLaunchKernelGGL((k_moe_gate_up_silu<__bf16, EMBER_MOE_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
   }
   return launch_status();
 }
