@@ -7,10 +7,12 @@ residual-add + RMSNorm at hidden 4096. Inputs are resident in HBM; consecutive s
 rotate through enough input sets (> 1 GiB) that no step finds its data in the 256 MB
 Infinity Cache. `value` = algorithmic bytes of the chain / time per step (GB/s).
 
-Also printed in the same JSON line:
+Printed before the JSON line, one short `row cfg=...` line each (and in full with --full-out):
   per_op        every BASELINE configuration: GPU us per launch, achieved GB/s, % of
                 8 TB/s (algorithmic bytes; inputs rotated past the Infinity Cache;
-                back-to-back launches timed with hipEvents)
+                back-to-back launches timed with hipEvents), plus copy-ceiling rows: the
+                same bytes moved by a plain identity gather
+Also in the JSON line:
   us_per_layer  config 4 summed per T, plus the full per-layer elementwise set
   graph_replay  the Qwen3-8B per-layer kernels of all 36 layers recorded in one hipGraph
                 (torch.cuda.graph) and replayed, against eager launches (wall us per layer)
@@ -447,6 +449,17 @@ def _ops(torch, ops, tables):
         return (torch.arange(32768, device=dev), randn((32768, 4096), bf, 7000 + i))
     out.append(Op("copy_calibration", "cal", "identity gather [32768,4096] bf16 (256 MiB)", 2 * 2 ** 28,
                   copy_cal, lambda a: ops.embedding_hip(a[0], a[1]), 2 * 2 ** 28))
+
+    # Copy ceilings: the same kernel as an identity gather (ids 0..n-1, contiguous rows) at
+    # the traffic of the small BASELINE rows, so each row can be read against a plain copy
+    # of its own size in the same run (rope T=4096: 67 MB; embedding T=8192: 134 MB; MLA
+    # T=8192: 52 MB).
+    for rows, label in ((4096, "rope T=4096"), (8192, "embedding T=8192"), (3204, "MLA T=8192")):
+        def copy_ceil(i, rows=rows):
+            return (torch.arange(rows, device=dev), randn((rows, 4096), bf, 7100 + i))
+        out.append(Op("copy_ceiling", "ceil", f"identity gather [{rows},4096] bf16 (size of {label})",
+                      rows * (8 + 2 * 4096 * 2), copy_ceil, lambda a: ops.embedding_hip(a[0], a[1]),
+                      rows * 4096 * 2))
     return out
 
 
@@ -750,6 +763,7 @@ def main() -> int:
     ap.add_argument("--max-sets", type=int, default=512, help="cap on rotated input sets per op (profiler runs)")
     ap.add_argument("--configs", default=None, help="comma list of config labels to keep in the per-op rows")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--full-out", default=None, help="also write the full result (every per-op field) here")
     ap.add_argument("--only", default=None, help="comma list of ops: run only their per-op rows (profiler runs)")
     args = ap.parse_args()
 
@@ -921,7 +935,17 @@ def main() -> int:
         "graph_replay": graph_rows,
         "per_op": per_op,
     }
-    print(json.dumps(result))
+    if args.full_out:
+        Path(args.full_out).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.full_out).write_text(json.dumps(result, indent=1))
+    # Compact output: one short line per per-op row, then the JSON line (with per_op as
+    # short strings), so that every row survives a tail-limited capture of stdout.
+    for r in per_op:
+        cpu_s = f" cpu {r['cpu_GB/s']}GB/s" if "cpu_GB/s" in r else ""
+        print(f"row cfg={r['config']} {r['op']} {r['shape']}: {r['us']}us {r['GB/s']}GB/s "
+              f"{r['pct_peak']}%{cpu_s}")
+    result["per_op"] = f"{len(per_op)} rows, printed above as 'row cfg=...' lines"
+    print(json.dumps(result), flush=True)
     return 0
 
 

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -23,6 +23,7 @@ ERR_DECODE_CTX = 8
 ERR_BLOCK_ID = 16
 ERR_ROW_INDEX = 32
 ERR_SYNC = 64
+ERR_EXPERT_ID = 128
 DECODE_FP32 = 1
 
 _DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -67,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "ember_moe_gate_up_silu": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
                                _i64, _p, _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],
+    "ember_moe_align_padded_size": [_i64, _i64, _i64],
+    "ember_moe_align": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],
@@ -75,7 +78,8 @@ SIGNATURES: dict[str, list] = {
 _RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspace_bytes": ctypes.c_int64,
             "ember_mla_decode_workspace_bytes": ctypes.c_int64,
             "ember_gate_up_silu_workspace_bytes": ctypes.c_int64,
-            "ember_moe_gate_up_silu_workspace_bytes": ctypes.c_int64}
+            "ember_moe_gate_up_silu_workspace_bytes": ctypes.c_int64,
+            "ember_moe_align_padded_size": ctypes.c_int64}
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:

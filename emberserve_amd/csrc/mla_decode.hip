@@ -179,7 +179,7 @@ __device__ __forceinline__ void split_range(int ctx, int splits, int split, int&
 template <typename T, int DL, int NP>
 __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds, float m, float lsum,
                                            const f32x4 (&o)[DL / 32], int b, int split, int head0,
-                                           int nhc) {
+                                           int nhc, bool poisoned = false) {
   constexpr int NDT = DL / 32;
   struct Combine {
     float m[NP][16];
@@ -195,7 +195,11 @@ __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds,
   // merge the tile streams (the two waves of a pair hold the same m and l)
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
+  // any poisoned wave (a handshake that ran out) poisons every row of the workgroup
+  __shared__ int any_poisoned;
+  if (threadIdx.x == 0) any_poisoned = 0;
   __syncthreads();
+  if (poisoned && lane == 0) any_poisoned = 1;
   Combine& cb = *reinterpret_cast<Combine*>(lds);
   if (g == 0 && hw == 0) {
     cb.m[pr][n] = m;
@@ -229,6 +233,7 @@ __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds,
       mw[v] = cb.m[v][hh];
       mx = fmaxf(mx, mw[v]);
     }
+    if (any_poisoned) mx = __builtin_nanf("");
 #pragma unroll
     for (int v = 0; v < NP; ++v) {
       const float wt = mw[v] == -INFINITY ? 0.f : exp2_fast(mw[v] - mx);
@@ -328,6 +333,15 @@ __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds,
     gm = cm;
   }
   if (mine) store_out(gl);
+}
+
+// Poisons a wave's online-softmax state (running max, sum, accumulators) with NaN.
+template <int NDT>
+__device__ __forceinline__ void poison_state(float& m, float& lsum, f32x4 (&o)[NDT]) {
+  m = __builtin_nanf("");
+  lsum = __builtin_nanf("");
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4{m, m, m, m};
 }
 
 template <typename T, int DL, int DR, int NP, bool PSYNC>
@@ -581,7 +595,11 @@ k_mla_mfma(MlaArgs a) {
     if constexpr (!PSYNC) __syncthreads();
   }
 
-  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc);
+  // A wave whose handshake ran out has read stale partner scores: its state is poisoned, so
+  // the output rows of this workgroup (or the merge of its split) come out NaN instead of a
+  // plausible wrong value, next to the EMBER_ERR_SYNC bit.
+  if (!sync_ok) poison_state(m, lsum, o);
+  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc, !sync_ok);
 }
 
 // k_mla_lds: the small-grid form of k_mla_mfma (same work split: two wave pairs per
@@ -832,7 +850,11 @@ k_mla_lds(MlaArgs a) {
       for (int kk = 0; kk < PVB; ++kk) o[d0 + kk] = M::run(__builtin_bit_cast(V8, va[kk]), pb, o[d0 + kk]);
     }
   }
-  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc);
+  // A wave whose handshake ran out has read stale partner scores: its state is poisoned, so
+  // the output rows of this workgroup (or the merge of its split) come out NaN instead of a
+  // plausible wrong value, next to the EMBER_ERR_SYNC bit.
+  if (!sync_ok) poison_state(m, lsum, o);
+  mla_finish<T, DL, NP>(a, lds, m, lsum, o, b, split, head0, nhc, !sync_ok);
 }
 
 constexpr int kAnyMaxD = 1024;          // DL + DR of the fp32 kernel

@@ -32,7 +32,8 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib, ops
-from .ops import _launch, _require_device, fused_enabled
+from ._scratch import ScratchCache, round_up
+from .ops import _check_indices, _launch, _require_device, fused_enabled
 from .paged_decode import num_sms
 
 MAX_TOKENS = 64    # the kernel's limit
@@ -48,26 +49,14 @@ def gate_up_silu_workgroups(device: torch.device) -> int:
     return num_sms(device)
 
 
-class _Scratch:
-    """Partials and arrival counters, zero-filled once and cached per (workgroups, token
-    tile count, hidden, inter, device) so graph replays see captured addresses."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple, Tensor] = {}
-
-    def get(self, programs: int, tokens: int, hidden: int, inter: int, device: torch.device) -> Tensor:
-        key = (programs, -(-tokens // 16), hidden, inter, str(device))
-        buf = self._bufs.get(key)
-        if buf is None:
-            nbytes = _lib.load().ember_gate_up_silu_workspace_bytes(16 * key[1], hidden, inter, programs)
-            if nbytes < 0:
-                raise ValueError(f"gate_up_silu: no plan for hidden {hidden}, inter {inter}, {programs} workgroups")
-            buf = torch.zeros(max(nbytes, 256) // 4, dtype=torch.float32, device=device)
-            self._bufs[key] = buf
-        return buf
+def _workspace_bytes(programs: int, tiles: int, hidden: int, inter: int) -> int:
+    return _lib.load().ember_gate_up_silu_workspace_bytes(16 * tiles, hidden, inter, programs)
 
 
-_SCRATCH = _Scratch()
+# Partials and arrival counters, zero-filled once and cached per (workgroups, token tile
+# count, hidden, inter, device, stream) so graph replays see captured addresses and two
+# streams never share counters.
+_SCRATCH = ScratchCache("gate_up_silu")
 
 
 def gate_up_silu_torch(x: Tensor, weight: Tensor) -> Tensor:
@@ -106,8 +95,12 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     programs = gate_up_silu_workgroups(x.device) if num_workgroups is None else int(num_workgroups)
     if programs < 1:
         raise ValueError(f"gate_up_silu: num_workgroups must be >= 1, got {programs}")
-    ws = _SCRATCH.get(programs, T, H, I, x.device)
+    tiles = -(-T // 16)
+    ws = _SCRATCH.get((programs, tiles, H, I), lambda: _workspace_bytes(programs, tiles, H, I), x.device)
     _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
             x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
             T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+    if _check_indices():
+        need, slabs = _workspace_bytes(programs, tiles, H, I), I // SLAB
+        _SCRATCH.verify_counters(ws, need - round_up(slabs * 4, 256), need - round_up(slabs * 4, 256) + slabs * 4)
     return out.view(*x.shape[:-1], I)

@@ -27,6 +27,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from ._scratch import ScratchCache, round_up
 from .ops import _check_indices, _launch, _require_device
 from .paged_decode import num_sms
 
@@ -60,26 +61,14 @@ def mla_num_splits(batch: int, device: torch.device, *, num_heads: int = 16,
     return max(1, min(MAX_SPLITS, want))
 
 
-class _Scratch:
-    """Split-K partial buffers, cached per (num_splits, B, H, DL, device) so a graph replay
-    reads the addresses that were captured (the reference's _SCRATCH)."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple, Tensor] = {}
-
-    def get(self, num_splits: int, batch: int, num_heads: int, dl: int, device: torch.device) -> Tensor:
-        key = (num_splits, batch, num_heads, dl, str(device))
-        buf = self._bufs.get(key)
-        if buf is None:
-            nbytes = _lib.load().ember_mla_decode_workspace_bytes(batch, num_heads, dl, num_splits)
-            # zero-filled once: the arrival counters at its end start at zero and every call
-            # leaves them there
-            buf = torch.zeros(max(nbytes, 16) // 4, dtype=torch.float32, device=device)
-            self._bufs[key] = buf
-        return buf
+def _workspace_bytes(num_splits: int, batch: int, num_heads: int, dl: int) -> int:
+    return _lib.load().ember_mla_decode_workspace_bytes(batch, num_heads, dl, num_splits)
 
 
-_SCRATCH = _Scratch()
+# Split-K partials and arrival counters, cached per (num_splits, B, H, DL, device, stream) so
+# a graph replay reads the addresses that were captured (the reference's _SCRATCH) and two
+# streams never share counters.
+_SCRATCH = ScratchCache("mla_decode", min_bytes=16)
 
 
 def mla_decode_torch(q_c: Tensor, q_pe: Tensor, latent_cache: Tensor, block_tables: Tensor,
@@ -142,7 +131,9 @@ def mla_decode(q_abs: Tensor | tuple[Tensor, Tensor], latent_cache: Tensor, bloc
     if num_splits is None:
         num_splits = mla_num_splits(B, q_c.device, num_heads=H, max_context=max_context)
     num_splits = max(1, min(int(num_splits), num_tiles_max))
-    ws = _SCRATCH.get(num_splits, B, H, DL, q_c.device) if num_splits > 1 else None
+    ws = None
+    if num_splits > 1:
+        ws = _SCRATCH.get((num_splits, B, H, DL), lambda: _workspace_bytes(num_splits, B, H, DL), q_c.device)
     _launch("ember_mla_decode", _lib.load().ember_mla_decode, q_c.device,
             q_c.data_ptr(), q_c.stride(0), q_c.stride(1), q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1),
             _lib.dtype_tag(q_c.dtype), latent_cache.data_ptr(), num_blocks, block_size, DL, DR,
@@ -152,11 +143,22 @@ def mla_decode(q_abs: Tensor | tuple[Tensor, Tensor], latent_cache: Tensor, bloc
             ws.data_ptr() if ws is not None else None, ws.numel() * 4 if ws is not None else 0,
             out.data_ptr(), out.stride(0), out.stride(1))
     if _check_indices():
-        flags = _lib.read_errors(clear=True)
-        if flags & _lib.ERR_DECODE_CTX:
-            raise IndexError("emberserve_amd.mla_decode: context length outside the block table")
-        if flags & _lib.ERR_BLOCK_ID:
-            raise IndexError("emberserve_amd.mla_decode: block id outside the cache")
-        if flags & _lib.ERR_SYNC:
-            raise RuntimeError("emberserve_amd.mla_decode: an in-kernel wave handshake timed out")
+        if ws is not None:
+            need = _workspace_bytes(num_splits, B, H, DL)
+            start = need - round_up(B * H * 4, 16)
+            _SCRATCH.verify_counters(ws, start, start + B * H * 4)
+        raise_decode_errors(_lib.read_errors(clear=True))
     return out
+
+
+def raise_decode_errors(flags: int) -> None:
+    """Maps the device error word after an mla_decode launch to an exception. A handshake
+    that ran out (ERR_SYNC) has already turned the affected output rows into NaN in the
+    kernel; the bit says why."""
+    if flags & _lib.ERR_DECODE_CTX:
+        raise IndexError("emberserve_amd.mla_decode: context length outside the block table")
+    if flags & _lib.ERR_BLOCK_ID:
+        raise IndexError("emberserve_amd.mla_decode: block id outside the cache")
+    if flags & _lib.ERR_SYNC:
+        raise RuntimeError("emberserve_amd.mla_decode: an in-kernel wave handshake timed out; the rows of "
+                           "the affected workgroups were written as NaN")

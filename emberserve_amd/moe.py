@@ -21,6 +21,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib, ops
+from ._scratch import ScratchCache, round_up
 from .ops import _check_indices, _launch, _require_device, fused_enabled
 from .paged_decode import num_sms
 
@@ -28,30 +29,52 @@ BLOCK_M = 16  # assignments per block (moe_triton.py:38)
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
 
 
-def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tuple[Tensor, Tensor, int]:
-    """The block-aligned expert layout of moe_triton.py:215-254, as device-side torch ops
-    (no host sync). Returns (sorted_ids [max_padded] int32, block_expert [max_blocks]
-    int32, num_valid): assignments id = token * k + choice grouped by expert in ascending
-    id order, each expert's run padded to a multiple of block_m with num_valid, and the
-    expert of every block (num_experts past the last used block)."""
-    n, k = topk_ids.shape
-    num_valid = n * k
-    dev = topk_ids.device
-    flat = topk_ids.reshape(-1).long()
+def moe_align_torch(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tuple[Tensor, Tensor, int]:
+    """Eager form of the layout for CPU tensors: one pass per expert over the flat
+    assignment list (nonzero gives each expert's ids in ascending order)."""
+    flat = topk_ids.reshape(-1)
+    num_valid = flat.numel()
     max_padded = -(-(num_valid + num_experts * (block_m - 1)) // block_m) * block_m
-    max_blocks = max_padded // block_m
-    order = torch.argsort(flat, stable=True)
-    expert_of = flat[order]
-    counts = torch.zeros(num_experts, dtype=torch.long, device=dev)
-    counts.scatter_add_(0, flat, torch.ones_like(flat))
-    padded = -(-counts // block_m) * block_m
-    pad_start = torch.cumsum(padded, 0) - padded
-    first = torch.cumsum(counts, 0) - counts
-    pos = pad_start[expert_of] + torch.arange(num_valid, device=dev) - first[expert_of]
-    sorted_ids = torch.full((max_padded,), num_valid, dtype=torch.int32, device=dev)
-    sorted_ids[pos] = order.to(torch.int32)
-    block_end = torch.cumsum(padded, 0) // block_m
-    block_expert = torch.searchsorted(block_end, torch.arange(max_blocks, device=dev), right=True).to(torch.int32)
+    sorted_ids = torch.full((max_padded,), num_valid, dtype=torch.int32, device=flat.device)
+    block_expert = torch.full((max_padded // block_m,), num_experts, dtype=torch.int32, device=flat.device)
+    at = 0
+    for e in range(num_experts):
+        mine = (flat == e).nonzero().view(-1)
+        n = mine.numel()
+        if n == 0:
+            continue
+        sorted_ids[at:at + n] = mine.to(torch.int32)
+        nb = -(-n // block_m)
+        block_expert[at // block_m:at // block_m + nb] = e
+        at += nb * block_m
+    return sorted_ids, block_expert, num_valid
+
+
+def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tuple[Tensor, Tensor, int]:
+    """The block-aligned expert layout of moe_triton.py:215-254 (the single-launch form of
+    :97-160): one launch of `ember_moe_align` on the GPU, no host sync, no workspace.
+    Returns (sorted_ids [max_padded] int32, block_expert [max_blocks] int32, num_valid):
+    assignments id = token * k + choice grouped by expert in ascending id order, each
+    expert's run padded to a multiple of block_m with num_valid, and the expert of every
+    block (num_experts past the last used block). CPU tensors take `moe_align_torch`."""
+    flat = topk_ids.reshape(-1)
+    if not flat.is_cuda:
+        return moe_align_torch(topk_ids, num_experts, block_m)
+    if flat.dtype not in (torch.int32, torch.int64):
+        flat = flat.long()
+    flat = flat.contiguous()
+    num_valid = flat.numel()
+    lib = _lib.load()
+    max_padded = lib.ember_moe_align_padded_size(num_valid, num_experts, block_m)
+    if max_padded < 0:
+        raise ValueError(f"moe_align: bad sizes (num_valid {num_valid}, num_experts {num_experts}, "
+                         f"block_m {block_m})")
+    sorted_ids = torch.empty((max_padded,), dtype=torch.int32, device=flat.device)
+    block_expert = torch.empty((max_padded // block_m,), dtype=torch.int32, device=flat.device)
+    _launch("ember_moe_align", lib.ember_moe_align, flat.device, flat.data_ptr(), flat.element_size(), num_valid,
+            num_experts, block_m, sorted_ids.data_ptr(), max_padded, block_expert.data_ptr(), max_padded // block_m)
+    if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_EXPERT_ID:
+        raise IndexError(f"emberserve_amd.moe_align: expert id outside [0, {num_experts})")
     return sorted_ids, block_expert, num_valid
 
 
@@ -68,26 +91,14 @@ def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, de
     return 1
 
 
-class _Scratch:
-    """Split partials and counters, zero-filled once per (splits, num_valid, inter,
-    num_blocks, device), so graph replays see captured addresses."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple, Tensor] = {}
-
-    def get(self, splits: int, num_valid: int, inter: int, num_blocks: int, device: torch.device) -> Tensor:
-        key = (splits, num_valid, inter, num_blocks, str(device))
-        buf = self._bufs.get(key)
-        if buf is None:
-            nbytes = _lib.load().ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, splits)
-            if nbytes < 0:
-                raise ValueError(f"moe_gate_up_silu: no workspace for {splits} splits, {num_valid} rows")
-            buf = torch.zeros(max(nbytes, 256) // 4, dtype=torch.float32, device=device)
-            self._bufs[key] = buf
-        return buf
+def _workspace_bytes(splits: int, num_valid: int, inter: int, num_blocks: int) -> int:
+    return _lib.load().ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, splits)
 
 
-_SCRATCH = _Scratch()
+# Split partials and counters, zero-filled once per (splits, num_valid, inter, num_blocks,
+# device, stream), so graph replays see captured addresses and two streams never share
+# counters.
+_SCRATCH = ScratchCache("moe_gate_up_silu")
 
 
 def moe_gate_up_silu_torch(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor,
@@ -136,14 +147,22 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
     if num_splits not in (1, 2, 4) or (H // 64) % num_splits or H // 64 // num_splits < 2:
         raise ValueError(f"moe_gate_up_silu: num_splits {num_splits} must be 1, 2 or 4 and divide hidden / 64 "
                          f"= {H // 64} with >= 2 steps per split")
-    ws = _SCRATCH.get(num_splits, num_valid, inter, block_expert.numel(), x.device) if num_splits > 1 else None
+    nb = block_expert.numel()
+    ws = None
+    if num_splits > 1:
+        ws = _SCRATCH.get((num_splits, num_valid, inter, nb), lambda: _workspace_bytes(num_splits, num_valid, inter, nb),
+                          x.device)
     _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
             x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
             _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
             block_expert.numel(), num_valid, top_k, num_splits, ws.data_ptr() if ws is not None else None,
             ws.numel() * 4 if ws is not None else 0, out.data_ptr(), out.stride(0))
-    if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
-        raise IndexError("emberserve_amd.moe_gate_up_silu: assignment id past the token rows")
+    if _check_indices():
+        if ws is not None:
+            need, cnt = _workspace_bytes(num_splits, num_valid, inter, nb), nb * (inter // 64)
+            _SCRATCH.verify_counters(ws, need - round_up(cnt * 4, 256), need - round_up(cnt * 4, 256) + cnt * 4)
+        if _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
+            raise IndexError("emberserve_amd.moe_gate_up_silu: assignment id past the token rows")
     return out
 
 

@@ -25,6 +25,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from ._scratch import ScratchCache, round_up
 from .ops import _check_indices, _launch, _require_device
 
 BLOCK_MULTIPLE = 16
@@ -109,26 +110,14 @@ def default_variant() -> str:
     return v
 
 
-class _Scratch:
-    """Split-K partial buffers, cached per (num_splits, B, H, D, device) so a graph replay
-    reads the addresses that were captured (paged_triton.py:293-310)."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple, Tensor] = {}
-
-    def get(self, num_splits: int, batch: int, num_heads: int, head_dim: int, device: torch.device) -> Tensor:
-        key = (num_splits, batch, num_heads, head_dim, str(device))
-        buf = self._bufs.get(key)
-        if buf is None:
-            nbytes = _lib.load().ember_paged_decode_workspace_bytes(batch, num_heads, head_dim, num_splits)
-            # zero-filled once: the arrival counters at its end start at zero and every
-            # call leaves them there
-            buf = torch.zeros(max(nbytes, 16) // 4, dtype=torch.float32, device=device)
-            self._bufs[key] = buf
-        return buf
+def _workspace_bytes(num_splits: int, batch: int, num_heads: int, head_dim: int) -> int:
+    return _lib.load().ember_paged_decode_workspace_bytes(batch, num_heads, head_dim, num_splits)
 
 
-_SCRATCH = _Scratch()
+# Split-K partials and arrival counters, cached per (num_splits, B, H, D, device, stream) so a
+# graph replay reads the addresses that were captured (paged_triton.py:293-310) and two
+# streams never share counters.
+_SCRATCH = ScratchCache("paged_attention_decode", min_bytes=16)
 
 
 def paged_decode_torch(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor,
@@ -190,7 +179,9 @@ def paged_attention_decode(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_ta
     if num_splits is None:
         num_splits = default_num_splits(B, Hkv, max_context, q.device, H, D)
     num_splits = max(1, min(int(num_splits), num_tiles_max))
-    ws = _SCRATCH.get(num_splits, B, H, D, q.device) if num_splits > 1 else None
+    ws = None
+    if num_splits > 1:
+        ws = _SCRATCH.get((num_splits, B, H, D), lambda: _workspace_bytes(num_splits, B, H, D), q.device)
     flags = _lib.DECODE_FP32 if variant == "sum" else 0
     _launch("ember_paged_decode", _lib.load().ember_paged_decode, q.device,
             q.data_ptr(), q.stride(0), q.stride(1), _lib.dtype_tag(q.dtype),
@@ -202,6 +193,9 @@ def paged_attention_decode(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_ta
             ws.data_ptr() if ws is not None else None, ws.numel() * 4 if ws is not None else 0,
             out.data_ptr(), out.stride(0), out.stride(1))
     if _check_indices():
+        if ws is not None:
+            need = _workspace_bytes(num_splits, B, H, D)
+            _SCRATCH.verify_counters(ws, need - round_up(B * H * 4, 16), need - round_up(B * H * 4, 16) + B * H * 4)
         flags = _lib.read_errors(clear=True)
         if flags & _lib.ERR_DECODE_CTX:
             raise IndexError("emberserve_amd.paged_attention_decode: context length outside the block table")

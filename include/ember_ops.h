@@ -87,6 +87,7 @@ extern "C" {
 #define EMBER_ERR_BLOCK_ID 16u  /* a block-table entry outside [0, num_blocks) */
 #define EMBER_ERR_ROW_INDEX 32u /* a row index past the end in ember_gather_rows / ember_scatter_rows2 */
 #define EMBER_ERR_SYNC 64u      /* an in-kernel wave handshake timed out (a library fault, never input) */
+#define EMBER_ERR_EXPERT_ID 128u /* an expert id outside [0, num_experts) in ember_moe_align */
 
 /* ABI version, bumped when an entry point is added or its signature changes. */
 int ember_abi_version(void);
@@ -378,6 +379,26 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
  * arrival counter per (block, 64-column slab). */
 int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter, int64_t num_blocks,
                                                int64_t num_splits);
+
+/* Slots of the block-aligned expert layout: round_up(num_valid + num_experts (block_m - 1),
+ * block_m), -1 for invalid arguments (the max_padded of moe_triton.py:249). */
+int64_t ember_moe_align_padded_size(int64_t num_valid, int64_t num_experts, int64_t block_m);
+
+/* The routed experts' block-aligned layout in one launch (one workgroup), replacing
+ * moe_align of emberserve/model/moe_triton.py:215-254 (its single-launch form is
+ * _moe_align_kernel, :97-160). topk_ids: num_valid = tokens * top_k expert ids (id_bytes 4
+ * or 8, contiguous, assignment id = position). Writes
+ *   sorted_ids [max_padded]: each expert's assignment ids in ascending order, its run padded
+ *     with num_valid to a multiple of block_m, experts in ascending order, num_valid after
+ *     the last run;
+ *   block_expert [max_blocks = max_padded / block_m]: the expert of each block, num_experts
+ *     past the last used block.
+ * max_padded must equal ember_moe_align_padded_size(...). 1 <= num_experts <= 1024. An id
+ * outside [0, num_experts) is left out of the layout and sets EMBER_ERR_EXPERT_ID. No host
+ * synchronisation, no workspace, no memset: safe to capture in a HIP graph. */
+int ember_moe_align(const void* topk_ids, int id_bytes, int64_t num_valid, int64_t num_experts, int64_t block_m,
+                    int32_t* sorted_ids, int64_t max_padded, int32_t* block_expert, int64_t max_blocks,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,10 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
   moe_gate_up_silu             every token routed to one expert equals gate_up_silu with
                                that expert's weight, row by row; rows follow the assignment
                                order t * k + c; experts are picked by index, not position.
+  moe_align                    the reference's own layout case (tests/test_moe_triton.py:
+                               34-48) written out slot by slot; every assignment exactly once;
+                               runs ascending and block-aligned; sizes; all-one-expert and
+                               no-assignment cases in closed form.
 No function is left unpinned.
 """
 
@@ -115,6 +119,30 @@ def moe_gate_up_silu(x: torch.Tensor, topk_ids: torch.Tensor, w_gate_up: torch.T
         for c in range(k):
             rows.append(gate_up_silu(x[t:t + 1], w_gate_up[int(topk_ids[t, c])]))
     return torch.cat(rows, dim=0)
+
+
+def moe_align(topk_ids: torch.Tensor, num_experts: int, block_m: int) -> tuple[list, list, int]:
+    """The block-aligned expert layout that moe_align returns (emberserve/model/
+    moe_triton.py:215-254, contract in its docstring :217-228), defined assignment by
+    assignment: for experts in ascending order, the ids (token * k + choice) routed to the
+    expert in ascending order, padded with num_valid to a multiple of block_m; num_valid up
+    to max_padded = round_up(num_valid + E (block_m - 1), block_m) (:247); block b's expert
+    is the expert whose padded run holds slot b * block_m, num_experts past the last run.
+    Returns plain lists (sorted_ids, block_expert) and num_valid."""
+    flat = [int(v) for v in topk_ids.reshape(-1).tolist()]
+    num_valid = len(flat)
+    max_padded = (num_valid + num_experts * (block_m - 1) + block_m - 1) // block_m * block_m
+    sorted_ids, block_expert = [], []
+    for e in range(num_experts):
+        run = [i for i, v in enumerate(flat) if v == e]
+        if not run:
+            continue
+        pad = -len(run) % block_m
+        sorted_ids += run + [num_valid] * pad
+        block_expert += [e] * ((len(run) + pad) // block_m)
+    sorted_ids += [num_valid] * (max_padded - len(sorted_ids))
+    block_expert += [num_experts] * (max_padded // block_m - len(block_expert))
+    return sorted_ids, block_expert, num_valid
 
 
 def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

@@ -377,6 +377,8 @@ def test_moe_align_layout(n, e, k):
     ids = torch.randint(0, e, (n, k), generator=torch.Generator().manual_seed(n * e))
     sorted_ids, block_expert, nv = moe_align(ids, e)
     assert nv == n * k
+    want_s, want_b, _ = ref.moe_align(ids, e, BLOCK_M)
+    assert sorted_ids.tolist() == want_s and block_expert.tolist() == want_b
     max_padded = -(-(nv + e * (BLOCK_M - 1)) // BLOCK_M) * BLOCK_M
     assert sorted_ids.shape == (max_padded,) and block_expert.shape == (max_padded // BLOCK_M,)
     s = sorted_ids.tolist()

@@ -600,3 +600,50 @@ def test_moe_gate_up_silu_oracle_rows_and_experts():
     ids = torch.tensor([[1, 0]] * 4)
     got = ref.moe_gate_up_silu(x, ids, w)
     assert torch.equal(got[0::2], ref.gate_up_silu(x, w1)) and torch.equal(got[1::2], ref.gate_up_silu(x, w0))
+
+
+# ---- moe_align layout ---------------------------------------------------------------------
+def test_moe_align_oracle_reference_case():
+    """tests/test_moe_triton.py:34-48's case (N=4, k=2, E=4, block 4), slot by slot:
+    flat ids [1,3,3,0,1,1,3,2] -> expert 0 {3}, 1 {0,4,5}, 2 {7}, 3 {1,2,6}."""
+    ids = torch.tensor([[1, 3], [3, 0], [1, 1], [3, 2]])
+    s, b, nv = ref.moe_align(ids, 4, 4)
+    assert nv == 8
+    assert s == [3, 8, 8, 8, 0, 4, 5, 8, 7, 8, 8, 8, 1, 2, 6, 8, 8, 8, 8, 8]
+    assert b == [0, 1, 2, 3, 4]
+
+
+def test_moe_align_oracle_closed_forms():
+    # every assignment to one expert: one run 0..nv-1, then padding; that expert's blocks
+    ids = torch.full((5, 3), 2)
+    s, b, nv = ref.moe_align(ids, 8, 4)
+    assert nv == 15 and len(s) == (15 + 8 * 3 + 3) // 4 * 4
+    assert s[:15] == list(range(15)) and all(v == 15 for v in s[15:])
+    assert b[:4] == [2] * 4 and all(v == 8 for v in b[4:])
+    # no assignments: all sentinels
+    s, b, nv = ref.moe_align(torch.zeros((0, 6), dtype=torch.long), 64, 16)
+    assert nv == 0 and s == [0] * 960 and b == [64] * 60
+    # block 1: every assignment is its own block, in expert then id order
+    s, b, nv = ref.moe_align(torch.tensor([[2, 0], [2, 1]]), 3, 1)
+    assert s == [1, 3, 0, 2] and b == [0, 1, 2, 2]
+
+
+@pytest.mark.parametrize("n,e,k,bm", [(1, 64, 6, 16), (7, 8, 2, 16), (50, 16, 4, 16), (3, 4, 4, 4), (40, 5, 3, 8)])
+def test_moe_align_oracle_properties(n, e, k, bm):
+    """Each assignment exactly once; runs ascending, one expert each, starting on a block
+    boundary; blocks in ascending expert order; block counts ceil(count / bm)."""
+    ids = torch.randint(0, e, (n, k), generator=torch.Generator().manual_seed(n * e + k))
+    s, b, nv = ref.moe_align(ids, e, bm)
+    flat = ids.reshape(-1).tolist()
+    assert len(s) == -(-(nv + e * (bm - 1)) // bm) * bm and len(b) == len(s) // bm
+    assert sorted(v for v in s if v < nv) == list(range(nv))
+    used = [x for x in b if x < e]
+    assert used == sorted(used) and all(x == e for x in b[len(used):])
+    for x in range(e):
+        assert used.count(x) == -(-flat.count(x) // bm)
+    for blk, x in enumerate(b):
+        rows = [v for v in s[blk * bm:(blk + 1) * bm] if v < nv]
+        if x >= e:
+            assert not rows
+        else:
+            assert rows == sorted(rows) and all(flat[v] == x for v in rows)
