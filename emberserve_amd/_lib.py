@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -60,6 +60,10 @@ SIGNATURES: dict[str, list] = {
     "ember_paged_decode": [_p, _i64, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                            _i64, _i32, _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _i32, _p, _i64, _p, _i64,
                            _i64, _p],
+    "ember_paged_decode_noalloc_max_bytes": [],
+    "ember_paged_decode_noalloc": [_p, _i64, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, _i64, _i32, _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _i32, _p, _i64,
+                                   _i64, _p],
     "ember_mla_decode_workspace_bytes": [_i64, _i64, _i64, _i64],
     "ember_mla_decode": [_p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                          _p, _i64, _i64, _p, _i64, _i64, _f32, _i64, _p, _i64, _p, _i64, _i64, _p],
@@ -79,7 +83,8 @@ _RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspac
             "ember_mla_decode_workspace_bytes": ctypes.c_int64,
             "ember_gate_up_silu_workspace_bytes": ctypes.c_int64,
             "ember_moe_gate_up_silu_workspace_bytes": ctypes.c_int64,
-            "ember_moe_align_padded_size": ctypes.c_int64}
+            "ember_moe_align_padded_size": ctypes.c_int64,
+            "ember_paged_decode_noalloc_max_bytes": ctypes.c_int64}
 
 
 def load(path: Path | str | None = None) -> ctypes.CDLL:

@@ -38,6 +38,9 @@
 // Bad inputs never fault: a context length outside [0, max_blocks * block_size] is clamped
 // and sets EMBER_ERR_DECODE_CTX; a block id outside [0, num_blocks) reads block 0 and sets
 // EMBER_ERR_BLOCK_ID. A zero context gives 0/0 = NaN rows, as the reference kernel does.
+#include <atomic>
+#include <mutex>
+
 #include "ember_common.h"
 
 namespace ember {
@@ -714,15 +717,23 @@ int64_t ember_paged_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, 
   return partials + (num_seqs * num_heads * int64_t(sizeof(uint32_t)) + 15) / 16 * 16;
 }
 
-int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
-                       const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
-                       int64_t num_kv_heads, int64_t head_dim, int64_t k_block_stride, int64_t k_slot_stride,
-                       int64_t k_head_stride, int64_t v_block_stride, int64_t v_slot_stride,
-                       int64_t v_head_stride, int cache_dtype, const int32_t* block_tables,
-                       int64_t block_table_stride, int64_t max_blocks, const int32_t* context_lens,
-                       int64_t num_seqs, int64_t num_heads, float scale, int64_t num_splits, int flags,
-                       void* workspace, int64_t workspace_bytes, void* out, int64_t out_seq_stride,
-                       int64_t out_head_stride, void* stream) {
+}  // extern "C"
+
+namespace ember {
+namespace {
+
+// ember_paged_decode's body. `counters` (when non-null) replaces the arrival counters at the
+// end of the workspace: the no-allocation entry point keeps them at a fixed place, so that
+// calls of different shapes always find them at zero.
+int paged_decode_core(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
+                      const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
+                      int64_t num_kv_heads, int64_t head_dim, int64_t k_block_stride, int64_t k_slot_stride,
+                      int64_t k_head_stride, int64_t v_block_stride, int64_t v_slot_stride,
+                      int64_t v_head_stride, int cache_dtype, const int32_t* block_tables,
+                      int64_t block_table_stride, int64_t max_blocks, const int32_t* context_lens,
+                      int64_t num_seqs, int64_t num_heads, float scale, int64_t num_splits, int flags,
+                      void* workspace, int64_t workspace_bytes, uint32_t* counters, void* out,
+                      int64_t out_seq_stride, int64_t out_head_stride, void* stream) {
   const int qsz = dtype_size(q_dtype);
   const int csz = dtype_size(cache_dtype);
   if (qsz == 0 || csz == 0) return EMBER_EINVAL;
@@ -776,7 +787,7 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
     a.part_m = ws;
     a.part_l = ws + rows;
     a.part_o = ws + 2 * rows;
-    a.counters = reinterpret_cast<uint32_t*>(ws + rows * (head_dim + 2));
+    a.counters = counters != nullptr ? counters : reinterpret_cast<uint32_t*>(ws + rows * (head_dim + 2));
   }
   a.err = err;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -820,6 +831,111 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
     }
   }
   return launch_status();
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
+                       const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
+                       int64_t num_kv_heads, int64_t head_dim, int64_t k_block_stride, int64_t k_slot_stride,
+                       int64_t k_head_stride, int64_t v_block_stride, int64_t v_slot_stride,
+                       int64_t v_head_stride, int cache_dtype, const int32_t* block_tables,
+                       int64_t block_table_stride, int64_t max_blocks, const int32_t* context_lens,
+                       int64_t num_seqs, int64_t num_heads, float scale, int64_t num_splits, int flags,
+                       void* workspace, int64_t workspace_bytes, void* out, int64_t out_seq_stride,
+                       int64_t out_head_stride, void* stream) {
+  return paged_decode_core(q, q_seq_stride, q_head_stride, q_dtype, k_cache, v_cache, num_blocks, block_size,
+                           num_kv_heads, head_dim, k_block_stride, k_slot_stride, k_head_stride, v_block_stride,
+                           v_slot_stride, v_head_stride, cache_dtype, block_tables, block_table_stride, max_blocks,
+                           context_lens, num_seqs, num_heads, scale, num_splits, flags, workspace, workspace_bytes,
+                           nullptr, out, out_seq_stride, out_head_stride, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- the no-allocation variant
+//
+// ember_paged_decode_noalloc keeps its split-K partials and arrival counters in `scratch`, a
+// file-scope device array of kNoAllocScratchBytes that every GPU the library runs on holds
+// until the process ends. The host-side name of the array is not a device address: its
+// address on each device comes from hipGetSymbolAddress, resolved once per device with that
+// device current, and only that address reaches kernels. The arrival counters sit at the
+// array's start, at the same place for every shape, and the partials after them. The array
+// is cleared by a fill kernel once per device (the counters must start at zero); every call
+// leaves the counters it used at zero again, and calls that overlap on one GPU share the
+// array and race.
+namespace ember {
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;
+constexpr int64_t kNoAllocCounterBytes = int64_t(1) << 20;  // arrival counters: 256 Ki (sequence, head) rows
+constexpr int kNoAllocMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::atomic<void*> g_scratch_addr[kNoAllocMaxDevices];
+std::mutex g_scratch_init;
+
+__global__ void __launch_bounds__(256) k_zero_words(uint32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) p[i] = 0u;
+}
+
+// The current device's address of `scratch`, cleared on first use (on `st`); null on failure.
+void* scratch_address(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocMaxDevices) return nullptr;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_init);
+  p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return nullptr;
+  k_zero_words<<<1024, 256, 0, st>>>(static_cast<uint32_t*>(addr), kNoAllocScratchBytes / 4);
+  if (hipGetLastError() != hipSuccess) return nullptr;
+  g_scratch_addr[dev].store(addr, std::memory_order_release);
+  return addr;
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int64_t ember_paged_decode_noalloc_max_bytes(void) {
+  return ember::kNoAllocScratchBytes - ember::kNoAllocCounterBytes;
+}
+
+int ember_paged_decode_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
+                               const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
+                               int64_t num_kv_heads, int64_t head_dim, int64_t k_block_stride,
+                               int64_t k_slot_stride, int64_t k_head_stride, int64_t v_block_stride,
+                               int64_t v_slot_stride, int64_t v_head_stride, int cache_dtype,
+                               const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                               const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                               int64_t num_splits, int flags, void* out, int64_t out_seq_stride,
+                               int64_t out_head_stride, void* stream) {
+  const int64_t need = ember_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, num_splits);
+  if (need < 0) return EMBER_EINVAL;
+  // counters at the array's start (fixed, whatever the shape), partials after them
+  if (need > ember::kNoAllocScratchBytes - ember::kNoAllocCounterBytes ||
+      num_seqs * num_heads * int64_t(sizeof(uint32_t)) > ember::kNoAllocCounterBytes)
+    return EMBER_ETOOBIG;
+  unsigned char* base = nullptr;
+  if (need > 0 && num_seqs > 0) {
+    base = static_cast<unsigned char*>(ember::scratch_address(static_cast<hipStream_t>(stream)));
+    if (base == nullptr) return EMBER_ENODEV;
+  }
+  return ember::paged_decode_core(
+      q, q_seq_stride, q_head_stride, q_dtype, k_cache, v_cache, num_blocks, block_size, num_kv_heads, head_dim,
+      k_block_stride, k_slot_stride, k_head_stride, v_block_stride, v_slot_stride, v_head_stride, cache_dtype,
+      block_tables, block_table_stride, max_blocks, context_lens, num_seqs, num_heads, scale, num_splits, flags,
+      base != nullptr ? base + ember::kNoAllocCounterBytes : nullptr,
+      base != nullptr ? ember::kNoAllocScratchBytes - ember::kNoAllocCounterBytes : 0,
+      reinterpret_cast<uint32_t*>(base), out, out_seq_stride, out_head_stride, stream);
 }
 
 }  // extern "C"

@@ -45,7 +45,7 @@ __host__ int device_cu_count() {
 
 extern "C" {
 
-int ember_abi_version(void) { return 9; }
+int ember_abi_version(void) { return 10; }
 
 const char* ember_status_string(int status) {
   switch (status) {
@@ -54,6 +54,7 @@ const char* ember_status_string(int status) {
     case EMBER_EALIGN: return "misaligned operand";
     case EMBER_ELAUNCH: return "kernel launch failed";
     case EMBER_ENODEV: return "no HIP device or HIP runtime call failed";
+    case EMBER_ETOOBIG: return "the call needs more scratch than the no-allocation entry point holds";
     default: return "unknown status";
   }
 }

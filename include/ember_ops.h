@@ -78,6 +78,7 @@ extern "C" {
 #define EMBER_EALIGN 2      /* a fused entry point's operands are not 16-byte aligned: run the unfused ops */
 #define EMBER_ELAUNCH 3     /* the HIP launch itself failed */
 #define EMBER_ENODEV 4      /* no HIP device / runtime call failed */
+#define EMBER_ETOOBIG 5     /* a no-allocation entry point's call needs more scratch than it holds */
 
 /* bits of the device error word */
 #define EMBER_ERR_EMBED_ID 1u   /* a token id outside [0, vocab) */
@@ -300,6 +301,26 @@ int ember_paged_decode(const void* q, int64_t q_seq_stride, int64_t q_head_strid
                        const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
                        int64_t num_splits, int flags, void* workspace, int64_t workspace_bytes,
                        void* out, int64_t out_seq_stride, int64_t out_head_stride, void* stream);
+
+/* ember_paged_decode without a workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture that may not call hipMalloc, tight serving loops, harnesses that
+ * forbid allocation). No counterpart in the reference. The split-K partials and counters live
+ * in a library-owned 16 MiB device array per GPU, held until the process ends; a call whose
+ * ember_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, num_splits) exceeds
+ * ember_paged_decode_noalloc_max_bytes() (15 MiB, the part left beside the counters), or
+ * with more than 262144 (sequence, head) rows, returns EMBER_ETOOBIG and launches nothing. It calls no allocator. All calls on one GPU share
+ * the array: calls that overlap on one GPU (two streams, concurrent graph replays) race.
+ * Arguments and results are ember_paged_decode's. */
+int64_t ember_paged_decode_noalloc_max_bytes(void);
+int ember_paged_decode_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride, int q_dtype,
+                               const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t block_size,
+                               int64_t num_kv_heads, int64_t head_dim, int64_t k_block_stride,
+                               int64_t k_slot_stride, int64_t k_head_stride, int64_t v_block_stride,
+                               int64_t v_slot_stride, int64_t v_head_stride, int cache_dtype,
+                               const int32_t* block_tables, int64_t block_table_stride, int64_t max_blocks,
+                               const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                               int64_t num_splits, int flags, void* out, int64_t out_seq_stride,
+                               int64_t out_head_stride, void* stream);
 
 /* Bytes of workspace ember_mla_decode needs for num_splits > 1 (0 for one split), -1 for
  * invalid arguments: fp32 partials [splits][seqs][heads][kv_lora_rank + 2] and one uint32

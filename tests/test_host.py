@@ -435,3 +435,16 @@ def test_swiglu_mlp_module_matches_the_reference_composition():
     with torch.no_grad():
         want = mlp.down_proj(ref.silu_and_mul(mlp.gate_up_proj(x)))
         assert torch.equal(mlp(x), want)
+
+
+def test_noalloc_decode_rejects_oversize_calls_before_any_launch():
+    """ember_paged_decode_noalloc refuses, with EMBER_ETOOBIG and no HIP call, a call whose
+    split-K workspace would not fit beside its counters in the library's scratch array."""
+    lib = _lib.load()
+    cap = lib.ember_paged_decode_noalloc_max_bytes()
+    assert cap == 15 * 2 ** 20
+    assert lib.ember_paged_decode_workspace_bytes(1024, 32, 128, 4) > cap
+    p = ctypes.c_void_p(16)  # never dereferenced
+    st = lib.ember_paged_decode_noalloc(p, 4096, 128, 2, p, p, 4, 16, 8, 128, 16384, 1024, 128, 16384, 1024, 128,
+                                        2, p, 4, 4, p, 1024, 32, 0.088, 4, 0, p, 4096, 128, None)
+    assert st == 5 and b"no-allocation" in lib.ember_status_string(5)
