@@ -21,6 +21,9 @@ namespace ember {
 
 constexpr int kWave = 64;
 
+// The slot of a padding row in the paged-cache writes: skipped without an error.
+constexpr int64_t kPadSlot = -1;
+
 // ---------------------------------------------------------------- dtype conversion
 
 __device__ __forceinline__ float to_f32(float v) { return v; }

@@ -5,7 +5,9 @@
 //     k_cache.view(num_slots, Hkv, D).index_copy_(0, slots, k); same for v
 //   PagedLatentCache.write (emberserve/kv/cache.py:152-157):
 //     latent_cache.view(num_slots, latent_dim).index_copy_(0, slots, latent)
-// Bit-exact copies. A slot outside [0, num_slots) is skipped and sets EMBER_ERR_KV_SLOT
+// Bit-exact copies. Slot -1 marks a padding row (a graph replayed at a token bucket larger
+// than the real row count) and is skipped silently. Any other slot outside [0, num_slots) is
+// skipped and sets EMBER_ERR_KV_SLOT
 // (torch's index_copy_ raises there); duplicate slots leave one of the writers, as
 // index_copy_ does.
 //
@@ -41,7 +43,7 @@ k_kv_write(const uint8_t* __restrict__ k, int64_t kts, int64_t khs, const uint8_
   const uint8_t* src = (isk ? k + tok * kts + h * khs : v + tok * vts + h * vhs) + j * 16;
   const Unit16 x = load_stream<uint32_t, 4>(reinterpret_cast<const uint32_t*>(src));
   if (slot < 0 || slot >= num_slots) {
-    if (j == 0 && r == 0) atomicOr(err, EMBER_ERR_KV_SLOT);
+    if (j == 0 && r == 0 && slot != kPadSlot) atomicOr(err, EMBER_ERR_KV_SLOT);
     return;
   }
   uint8_t* dst = (isk ? kc : vc) + slot * css + h * chs + j * 16;
@@ -63,7 +65,7 @@ k_kv_write_any(const E* __restrict__ k, int64_t kts, int64_t khs, const E* __res
   if (tok >= ntok) return;
   const int64_t slot = slots[tok];
   if (slot < 0 || slot >= num_slots) {
-    if (lane == 0 && r == 0) atomicOr(err, EMBER_ERR_KV_SLOT);
+    if (lane == 0 && r == 0 && slot != kPadSlot) atomicOr(err, EMBER_ERR_KV_SLOT);
     return;
   }
   const bool isk = r < hk;
@@ -84,7 +86,7 @@ k_row_scatter(const uint8_t* __restrict__ src, int64_t src_stride, const int64_t
   const int64_t slot = slots[tok];
   const Unit16* s = reinterpret_cast<const Unit16*>(src + tok * src_stride);
   if (slot < 0 || slot >= num_slots) {
-    if (lane == 0) atomicOr(err, EMBER_ERR_KV_SLOT);
+    if (lane == 0 && slot != kPadSlot) atomicOr(err, EMBER_ERR_KV_SLOT);
     return;
   }
   Unit16* d = reinterpret_cast<Unit16*>(dst + slot * dst_stride);
@@ -110,7 +112,7 @@ k_row_scatter_any(const E* __restrict__ src, int64_t src_stride, const int64_t* 
   if (tok >= ntok) return;
   const int64_t slot = slots[tok];
   if (slot < 0 || slot >= num_slots) {
-    if (lane == 0) atomicOr(err, EMBER_ERR_KV_SLOT);
+    if (lane == 0 && slot != kPadSlot) atomicOr(err, EMBER_ERR_KV_SLOT);
     return;
   }
   for (int i = lane; i < n; i += kWave) dst[slot * dst_stride + i] = src[tok * src_stride + i];

@@ -226,7 +226,7 @@ k_rope_kv(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k
   }
   if (j == 0 && h == 0) {
     if (bad) atomicOr(err, EMBER_ERR_ROPE_POS);
-    if (!slot_ok) atomicOr(err, EMBER_ERR_KV_SLOT);
+    if (!slot_ok && slot != kPadSlot) atomicOr(err, EMBER_ERR_KV_SLOT);
   }
 }
 
@@ -521,7 +521,7 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
         const int64_t slot = slots[toks[u]];
         if (slot >= 0 && slot < num_slots) {
           crow = cache + slot * css;
-        } else if (live && lane == 0) {
+        } else if (live && lane == 0 && slot != kPadSlot) {
           atomicOr(err, EMBER_ERR_KV_SLOT);
         }
       }
@@ -714,7 +714,7 @@ k_mla_tok(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe
   if constexpr (CACHE) {
     if (slot >= 0 && slot < num_slots) {
       crow = cache + slot * css;
-    } else if (lane == 0) {
+    } else if (lane == 0 && slot != kPadSlot) {
       atomicOr(err, EMBER_ERR_KV_SLOT);
     }
   }

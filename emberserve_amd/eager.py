@@ -78,12 +78,20 @@ def mla_latent_rope_torch(c: torch.Tensor, k_pe: torch.Tensor, q_pe: torch.Tenso
     return q_rot, torch.cat([cn, k_rot.squeeze(1)], dim=-1)
 
 
+# The slot of a padding row (a step padded up to a captured token bucket): the cache writes
+# skip it. Any other out-of-range slot is an error, as in index_copy_.
+PAD_SLOT = -1
+
+
 def kv_cache_write_torch(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
                          k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     """emberserve/kv/cache.py:54-61 for one layer: index_copy_ of k and v into the flat
     [num_slots, Hkv, D] views of the caches."""
     slots = slot_mapping.to(device=k_cache.device, dtype=torch.long)
     flat = (-1, k.shape[1], k.shape[2])
+    keep = slots != PAD_SLOT  # padding rows of a bucketed step are not stored
+    if not bool(keep.all()):
+        slots, k, v = slots[keep], k[keep], v[keep]
     k_cache.view(flat).index_copy_(0, slots, k.to(k_cache.dtype))
     v_cache.view(flat).index_copy_(0, slots, v.to(v_cache.dtype))
 
@@ -91,4 +99,7 @@ def kv_cache_write_torch(k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.T
 def latent_cache_write_torch(latent: torch.Tensor, slot_mapping: torch.Tensor, cache: torch.Tensor) -> None:
     """emberserve/kv/cache.py:152-157 for one layer."""
     slots = slot_mapping.to(device=cache.device, dtype=torch.long)
+    keep = slots != PAD_SLOT
+    if not bool(keep.all()):
+        slots, latent = slots[keep], latent[keep]
     cache.view(-1, latent.shape[-1]).index_copy_(0, slots, latent.to(cache.dtype))

@@ -166,15 +166,23 @@ def rmsnorm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
 
 
 def fused_add_rmsnorm_hip(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
-                          eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """ops_triton.py:100-110. Returns (normed, new_residual); the inputs are not modified."""
+                          eps: float, *, out: torch.Tensor | None = None,
+                          residual_out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """ops_triton.py:100-110. Returns (normed, new_residual); the inputs are not modified.
+    `out` / `residual_out` (2-D [rows, H], unit inner stride) receive the results instead of
+    new tensors, for callers with static buffers (graph pieces); `residual_out` may be
+    `residual` itself (each row is read whole before it is written)."""
     _require_device("fused_add_rmsnorm", x, residual, weight)
     if residual.dtype != x.dtype or residual.shape != x.shape:
         raise ValueError("x and residual must share shape and dtype")
     x2 = _rows2d(x)
     r2 = _rows2d(residual)
-    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
-    new_res = torch.empty(r2.shape, dtype=x.dtype, device=x.device)
+    for name, t in (("out", out), ("residual_out", residual_out)):
+        if t is not None and (t.shape != x2.shape or t.dtype != x.dtype or t.stride(-1) != 1 or t.device != x.device):
+            raise ValueError(f"fused_add_rmsnorm: {name} must be a {tuple(x2.shape)} {x.dtype} tensor on "
+                             f"{x.device} with unit inner stride")
+    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device) if out is None else out
+    new_res = torch.empty(r2.shape, dtype=x.dtype, device=x.device) if residual_out is None else residual_out
     w, wtag = _weight_for(weight, x)
     if w.numel() != x2.shape[1]:
         raise ValueError(f"weight has {w.numel()} elements, rows have {x2.shape[1]}")
@@ -208,14 +216,20 @@ def rope_hip(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Ten
     return q, k
 
 
-def silu_and_mul_hip(x: torch.Tensor) -> torch.Tensor:
-    """ops_triton.py:127-134."""
+def silu_and_mul_hip(x: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ops_triton.py:127-134. `out` ([rows, I], unit inner stride) receives the result
+    instead of a new tensor."""
     _require_device("silu_and_mul", x)
     if x.shape[-1] % 2 != 0:  # the eager form fails the same way: halves of unequal size
         raise ValueError(f"silu_and_mul: last dim {x.shape[-1]} is not even")
     x2 = _rows2d(x)
     inter = x2.shape[-1] // 2
-    out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)
+    if out is not None:
+        if out.shape != (x2.shape[0], inter) or out.dtype != x.dtype or out.stride(-1) != 1 or out.device != x.device:
+            raise ValueError(f"silu_and_mul: out must be a ({x2.shape[0]}, {inter}) {x.dtype} tensor on {x.device} "
+                             "with unit inner stride")
+    else:
+        out = torch.empty((x2.shape[0], inter), dtype=x.dtype, device=x.device)
     if inter == 0 or x2.shape[0] == 0:
         return out.view(*x.shape[:-1], inter)
     _launch("ember_silu_and_mul", _lib.load().ember_silu_and_mul, x.device,

@@ -209,8 +209,9 @@ int ember_scatter_rows2(const void* src0, int64_t src0_rows, int64_t src0_row_st
  *   v_cache[slot_mapping[t], h, :] = v[t, h, :]        t < num_tokens, h < num_kv_heads
  * Bit-exact copies of head_dim elements of elem_bytes bytes. Strides are in elements; the
  * caches are [num_slots, ...] with slot stride cache_slot_stride and head stride
- * cache_head_stride (both caches share the geometry). A slot outside [0, num_slots) skips
- * that token and sets EMBER_ERR_KV_SLOT; with duplicate slots one writer wins, as with
+ * cache_head_stride (both caches share the geometry). Slot -1 marks a padding row (a step
+ * replayed at a larger token bucket) and is skipped silently; any other slot outside
+ * [0, num_slots) skips that token and sets EMBER_ERR_KV_SLOT; with duplicate slots one writer wins, as with
  * index_copy_. */
 int ember_kv_cache_write(const void* k, int64_t k_token_stride, int64_t k_head_stride,
                          const void* v, int64_t v_token_stride, int64_t v_head_stride,
@@ -230,7 +231,8 @@ int ember_latent_cache_write(const void* latent, int64_t latent_token_stride, in
 
 /* ember_mla_latent_rope fused with the paged latent-cache write that follows it
  * (PagedLatentCache.write): the latent rows are stored at cache[slot_mapping[t], :] (slot
- * stride cache_slot_stride, slots outside [0, num_slots) skipped with EMBER_ERR_KV_SLOT)
+ * stride cache_slot_stride; slot -1 skipped silently, other slots outside [0, num_slots)
+ * skipped with EMBER_ERR_KV_SLOT)
  * and, when latent != NULL, also to latent[t, :]. Needs 16-byte aligned operands;
  * otherwise returns EMBER_EALIGN and does nothing. */
 int ember_mla_latent_rope_cache(const void* c, int64_t c_token_stride, int64_t kv_lora_rank,
