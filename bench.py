@@ -394,6 +394,22 @@ def _ops(torch, ops, tables):
         out.append(Op("moe_gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts ({used} used), "
                       f"w[{ne},{2 * inter},{h}] bf16", nbytes, make,
                       lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k), ne * 2 * inter * h * 2))
+        # the same with the alignment launched each time (ember_moe_align + the grouped kernel)
+        out.append(Op("moe_align+gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts, align each call",
+                      nbytes, make, lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k),
+                      ne * 2 * inter * h * 2))
+
+    def moe_align_row(cfg, n, ne=64, k=6):
+        """ember_moe_align alone (moe_triton.py:215-254's layout in one launch): bytes are the
+        ids read plus the layout written."""
+        from emberserve_amd.moe import moe_align
+        g.manual_seed(330 + n)
+        ids = torch.stack([torch.randperm(ne, generator=g, device=dev)[:k] for _ in range(n)])
+        nv = n * k
+        padded = -(-(nv + ne * 15) // 16) * 16
+        nbytes = nv * 8 + padded * 4 + padded // 16 * 4
+        out.append(Op("moe_align", cfg, f"ids[{n},{k}] int64, {ne} experts, block 16", nbytes,
+                      lambda i: (ids,), lambda a: moe_align(a[0], ne), nbytes))
 
     add_norm("1", 256, 896, f16)
     rope("2", 256)
@@ -441,6 +457,8 @@ def _ops(torch, ops, tables):
         gate_up("mlp", t, 3584, 18944, "qwen2.5-7b")
     for n in (1, 8, 64):
         moe_gate_up("moe", n)
+    for n in (1, 64, 8192):
+        moe_align_row("moe", n)
 
     # Counter calibration (run only when named by --only): a plain 256 MiB row copy (the
     # embedding kernel with ids = 0..n-1), whose FETCH_SIZE / WRITE_SIZE readings give the
