@@ -364,7 +364,7 @@ def _ops(torch, ops, tables):
         """The dense MLP's gate_up projection + silu_and_mul (qwen2.py:60-61) at a decode
         batch: the fused kernel and the unfused pair (torch linear = hipBLASLt, then
         silu_and_mul) on the same inputs."""
-        from emberserve_amd.gate_up_silu import gate_up_silu, gate_up_silu_torch
+        from emberserve_amd.gate_up_silu import gate_up_silu, gate_up_silu_torch, pack_gate_up_weight
         wbytes = 2 * inter * hidden * 2
 
         def make(i):
@@ -375,6 +375,12 @@ def _ops(torch, ops, tables):
                       lambda a: gate_up_silu(a[0], a[1], fused=True), wbytes))
         out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
                       lambda a: gate_up_silu_torch(a[0], a[1]), wbytes))
+
+        def make_packed(i):  # the weight packed once, at load time, outside the timed region
+            x, w = make(i)
+            return x, w, pack_gate_up_weight(w)
+        out.append(Op("gate_up_silu_packed", cfg, shape + " (weight packed at load)", nbytes, make_packed,
+                      lambda a: gate_up_silu(a[0], a[1], fused=True, packed=a[2]), wbytes))
 
     def moe_gate_up(cfg, n):
         """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's

@@ -39,15 +39,20 @@
 #ifndef EMBER_GU_STAGES
 #define EMBER_GU_STAGES 3
 #endif
-// Token tiles (of 16) up to which every wave loads its own copy of x. Measured on MI355X
-// (persistent grid, one workgroup per CU): private and shared copies tie at 1-16 tokens;
-// at 32 tokens the shared copy is faster (Qwen3-8B 41.2 vs 41.9 us, Qwen2.5-7B 59.2 vs 61.4).
+// Register ring stages of the packed-weight dense kernel. Measured on MI355X at Qwen3-8B and
+// Qwen2.5-7B, 1 and 16 tokens: 3 and 4 stages tie, 6 and 8 are 1-5% slower.
+#ifndef EMBER_GU_PACKED_STAGES
+#define EMBER_GU_PACKED_STAGES 3
+#endif
 // Ring stages of the routed-expert kernel (one workgroup per block and slab, not persistent).
 // Measured at Moonlight's geometry: 2 stages (48 KB of LDS, three workgroups per CU) are
 // 5-10% slower than 3 at 1-64 tokens (8 tokens: 98.8 vs 89.6 us).
 #ifndef EMBER_MOE_STAGES
 #define EMBER_MOE_STAGES 3
 #endif
+// Token tiles (of 16) up to which every wave loads its own copy of x. Measured on MI355X
+// (persistent grid, one workgroup per CU): private and shared copies tie at 1-16 tokens;
+// at 32 tokens the shared copy is faster (Qwen3-8B 41.2 vs 41.9 us, Qwen2.5-7B 59.2 vs 61.4).
 #ifndef EMBER_GU_PRIVX_MT
 #define EMBER_GU_PRIVX_MT 1
 #endif
@@ -119,6 +124,14 @@ __device__ __host__ __forceinline__ int64_t gu_start(int64_t b, int64_t total, i
 __device__ __host__ __forceinline__ int64_t gu_owner(int64_t u, int64_t total, int64_t G) {
   return ((u + 1) * G - 1) / total;
 }
+// Where the packed weight layout keeps unit t of workgroup b's run, in units: runs hold q =
+// total / G or q + 1 units, so the t-th units of all workgroups (t < q) are stored side by
+// side in workgroup order, t-major, and the extra units of the longer runs follow, also in
+// workgroup order. At any moment the grid then reads one narrow window of the array.
+__device__ __host__ __forceinline__ int64_t gu_packed_pos(int64_t b, int64_t t, int64_t total, int64_t G) {
+  const int64_t q = total / G;
+  return t < q ? t * G + b : q * G + (gu_start(b, total, G) - b * q);
+}
 
 // A workgroup barrier that waits for this wave's LDS reads but not for its global loads
 // (__syncthreads() carries a workgroup fence, which waits for every outstanding load and
@@ -135,6 +148,145 @@ __device__ __forceinline__ void gu_barrier() {
 // whole), so two.
 constexpr int kGuMaxFlush = 2;
 
+// The part of a dense run shared by both load paths: the per-unit bookkeeping of the
+// persistent run (slab ends, partials of slabs shared with other workgroups), the epilogue,
+// and the end-of-run merge of shared slabs by their last contributor.
+template <typename T, int MT>
+struct GuRun {
+  static constexpr int kFloats = kGuWaves * MT * 2 * kWave * 4;  // one partial of a slab
+  const GuArgs& a;
+  int w, lane, n, g;
+  int64_t nk, total, G;
+  int64_t flushed0 = 0, flushed1 = 0;  // scalars, not an array: an indexed member array goes to scratch
+  int nflush = 0;
+  int64_t cur_slab, cur_k, cur_first;  // the current unit; first k step of its slab in this run
+
+  __device__ __forceinline__ GuRun(const GuArgs& args, int64_t u0) : a(args) {
+    lane = threadIdx.x & (kWave - 1);
+    w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    n = lane & 15;
+    g = lane >> 4;
+    nk = a.H / kGuBK;
+    total = static_cast<int64_t>(a.I / kGuSlab) * nk;
+    G = gridDim.x;
+    cur_slab = u0 / nk;
+    cur_k = u0 - cur_slab * nk;
+    cur_first = cur_k;
+  }
+
+  // Epilogue of slab `sl` from sums `v`: lane (n, g) holds D[row 4g + i][token 16 mt + n]
+  // of its wave's gate and up tiles, so output columns sl * 64 + 16 w + 4g + [0, 4).
+  __device__ __forceinline__ void emit(int64_t sl, const f32x4 (&v)[MT][2]) {
+    T* out = static_cast<T*>(a.out);
+    const int64_t col = sl * kGuSlab + w * kGuRows + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int tok = 16 * mt + n;
+      if (tok < a.T) {
+        Pack<T, 4> o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gf = round_to<T>(v[mt][0][i]);
+          const float uf = round_to<T>(v[mt][1][i]);
+          const float act = round_to<T>(gf / (1.0f + expf(-gf)));
+          o.v[i] = from_f32<T>(act * uf);
+        }
+        store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
+      }
+    }
+  }
+  // Where a slab's partials live: part p of slab sl (p = contributing workgroup's order).
+  __device__ __forceinline__ CoherentRsrc part_rsrc(int64_t sl, int64_t p) const {
+    return coherent_rsrc(a.part + (sl * a.max_parts + p) * kFloats, kFloats);
+  }
+  __device__ __forceinline__ int part_off(int mt, int gu) const {
+    return (((w * MT + mt) * 2 + gu) * kWave + lane) * 16;
+  }
+
+  // After unit j of nu: at a slab end, emit the slab (whole k range here) or leave its
+  // partial, and clear the sums. DRAIN: then wait for the stores (and everything else) in the
+  // same block, so no path into the next unit carries a pending store.
+  template <bool DRAIN = false>
+  __device__ __forceinline__ void end_unit(int j, int nu, f32x4 (&acc)[MT][2]) {
+    const bool slab_end = cur_k == nk - 1 || j == nu - 1;
+    if (!slab_end) {
+      ++cur_k;
+      return;
+    }
+    if (cur_first == 0 && cur_k == nk - 1) {
+      emit(cur_slab, acc);
+    } else {
+      const int64_t p = gu_owner(cur_slab * nk + cur_first, total, G) - gu_owner(cur_slab * nk, total, G);
+      const CoherentRsrc rs = part_rsrc(cur_slab, p);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int gu = 0; gu < 2; ++gu) store_coherent<4>(rs, part_off(mt, gu), acc[mt][gu]);
+      if (nflush == 0) {
+        flushed0 = cur_slab;
+        nflush = 1;
+      } else if (nflush == 1) {
+        flushed1 = cur_slab;
+        nflush = 2;
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ++cur_slab;
+    cur_k = 0;
+    cur_first = 0;
+    if (DRAIN) __builtin_amdgcn_s_waitcnt(0);
+  }
+
+  // Count this workgroup's partials in; the last contributor of a slab sums its partials in
+  // k order (so results do not depend on arrival order), emits it and returns the counter
+  // to zero for the next launch.
+  __device__ __forceinline__ void merge(int* last_flags) {
+    if (nflush == 0) return;  // uniform
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x < nflush) {
+      const int64_t sl = threadIdx.x == 0 ? flushed0 : flushed1;
+      const uint32_t parts =
+          static_cast<uint32_t>(gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1);
+      uint32_t* cnt = a.counters + sl;
+      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = prev == parts - 1;
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flags[threadIdx.x] = last;
+    }
+    __syncthreads();
+    for (int f = 0; f < nflush; ++f) {
+      if (!last_flags[f]) continue;  // uniform
+      const int64_t sl = f == 0 ? flushed0 : flushed1;
+      const int64_t parts = gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1;
+      f32x4 sum[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) sum[mt][0] = sum[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      constexpr int SB = 4;  // partials per batch of loads
+      for (int64_t p0 = 0; p0 < parts; p0 += SB) {
+        f32x4 v[SB][MT][2];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const CoherentRsrc rs = part_rsrc(sl, min<int64_t>(p0 + u, parts - 1));
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int gu = 0; gu < 2; ++gu)
+              v[u][mt][gu] = p0 + u < parts ? load_coherent<4>(rs, part_off(mt, gu)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int gu = 0; gu < 2; ++gu) sum[mt][gu] += v[u][mt][gu];
+      }
+      emit(sl, sum);
+    }
+  }
+};
+
 // PRIVX: every wave loads its own copy of a step's x rows (2 KiB per 16 tokens, from L2),
 // so the waves never wait for each other; otherwise the four waves share one copy and
 // meet at a barrier every step. Private copies cost XB load instructions per wave per
@@ -150,7 +302,6 @@ k_gate_up_silu(GuArgs a) {
   constexpr int WBYTES = kGuWaves * WB * 1024;
   constexpr int STAGE = WBYTES + (PRIVX ? kGuWaves : 1) * XB * 1024;
   constexpr int LPS = WB + XBW;                             // direct loads per wave per stage
-  constexpr int kFloats = kGuWaves * MT * 2 * kWave * 4;    // one partial of a slab
   static_assert(NS >= 2 && NS <= 4 && LPS * (NS - 1) < 64, "stages");
   __shared__ __attribute__((aligned(16))) unsigned char lds[NS * STAGE];
   __shared__ int last_flags[kGuMaxFlush];
@@ -231,38 +382,7 @@ k_gate_up_silu(GuArgs a) {
     }
   };
 
-  // Epilogue of slab `sl` from sums `v`: lane (n, g) holds D[row 4g + i][token 16 mt + n]
-  // of its wave's gate and up tiles, so output columns sl * 64 + 16 w + 4g + [0, 4).
-  T* out = static_cast<T*>(a.out);
-  auto emit = [&](int64_t sl, const f32x4 (&v)[MT][2]) {
-    const int64_t col = sl * kGuSlab + w * kGuRows + 4 * g;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int tok = 16 * mt + n;
-      if (tok < a.T) {
-        Pack<T, 4> o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gf = round_to<T>(v[mt][0][i]);
-          const float uf = round_to<T>(v[mt][1][i]);
-          const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-          o.v[i] = from_f32<T>(act * uf);
-        }
-        store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
-      }
-    }
-  };
-  // Where a slab's partials live: part p of slab sl (p = contributing workgroup's order).
-  auto part_rsrc = [&](int64_t sl, int64_t p) {
-    return coherent_rsrc(a.part + (sl * a.max_parts + p) * kFloats, kFloats);
-  };
-  auto part_off = [&](int mt, int gu) { return (((w * MT + mt) * 2 + gu) * kWave + lane) * 16; };
-
-  int64_t flushed[kGuMaxFlush];
-  int nflush = 0;
-  int64_t cur_slab = u0 / nk;
-  int64_t cur_k = u0 - cur_slab * nk;
-  int64_t cur_first = cur_k;  // first k step of the current slab in this run
+  GuRun<T, MT> run(a, u0);
 
   // The ring: loads of unit j + NS - 1 are issued once every wave is past unit j - 1 (whose
   // buffer they overwrite). Each wave waits for its own loads of a unit, then the barrier
@@ -282,73 +402,124 @@ k_gate_up_silu(GuArgs a) {
     }
     if (j + NS - 1 < nu) issue(j + NS - 1);
     compute(j);
-    const bool slab_end = cur_k == nk - 1 || j == nu - 1;
-    if (slab_end) {
-      if (cur_first == 0 && cur_k == nk - 1) {
-        emit(cur_slab, acc);  // the whole k range of this slab is here
-      } else {
-        const int64_t p = gu_owner(cur_slab * nk + cur_first, total, G) -
-                          gu_owner(cur_slab * nk, total, G);
-        const CoherentRsrc rs = part_rsrc(cur_slab, p);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int gu = 0; gu < 2; ++gu) store_coherent<4>(rs, part_off(mt, gu), acc[mt][gu]);
-        if (nflush < kGuMaxFlush) flushed[nflush++] = cur_slab;
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      ++cur_slab;
-      cur_k = 0;
-      cur_first = 0;
-    } else {
-      ++cur_k;
-    }
+    run.end_unit(j, nu, acc);
   }
-  if (nflush == 0) return;
+  run.merge(last_flags);
+}
 
-  // Count this workgroup's partials in; the last contributor of a slab merges it.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x < nflush) {
-    const int64_t sl = flushed[threadIdx.x];
-    const uint32_t parts =
-        static_cast<uint32_t>(gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1);
-    uint32_t* cnt = a.counters + sl;
-    const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == parts - 1;
-    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flags[threadIdx.x] = last;
-  }
-  __syncthreads();
-  for (int f = 0; f < nflush; ++f) {
-    if (!last_flags[f]) continue;  // uniform
-    const int64_t sl = flushed[f];
-    const int64_t parts = gu_owner(sl * nk + nk - 1, total, G) - gu_owner(sl * nk, total, G) + 1;
-    f32x4 sum[MT][2];
+// The packed form: the weights pre-arranged once, for a grid of G workgroups
+// (ember_gate_up_silu_pack_weight), so that every MFMA operand fragment a wave needs is one
+// contiguous KiB. Unit u = (slab, 64-k step j) is 16 contiguous KiB,
+//   unit[h][wave][part][lane][8]  (h: k32 half of the step; part 0 gate, 1 up; lane = 16 g + n
+//   holds row 64 slab + 16 wave + n of the part, k = 64 j + 32 h + 8 g + [0, 8))
+// and the units sit in the order of gu_packed_pos: the grid reads the array front to back,
+// one G * 16 KiB window at a time, each load instruction moving 1 KiB with 64 consecutive
+// 16-byte lanes, with no LDS. Measured on MI355X (Qwen3-8B, 201 MB): 35.0 us against 37.8
+// for the same kernel with each workgroup's run stored as one contiguous range, and 40.5
+// for k_gate_up_silu's direct-to-LDS stream of the unpacked rows. x comes from L2 in the
+// B-operand layout. NS register stages per wave (the loop is unrolled by NS so every ring
+// index is a compile-time constant).
+template <typename T, int MT, int NS>
+__global__ void __launch_bounds__(kGuWaves * kWave, 1)
+k_gate_up_silu_packed(GuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  static_assert(NS >= 2 && NS <= 8, "stages");
+  __shared__ int last_flags[kGuMaxFlush];
+  const int64_t nk = a.H / kGuBK;
+  const int64_t total = static_cast<int64_t>(a.I / kGuSlab) * nk;
+  const int64_t u0 = gu_start(blockIdx.x, total, gridDim.x);
+  const int nu = static_cast<int>(gu_start(blockIdx.x + 1, total, gridDim.x) - u0);  // >= 1
+  GuRun<T, MT> run(a, u0);
+  const int lane = run.lane, w = run.w, n = run.n, g = run.g;
+
+  const T* wp = static_cast<const T*>(a.w) + (w * 2 * kWave + lane) * 8;
+  const T* xg = static_cast<const T*>(a.x);
+  const T* xrow[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) sum[mt][0] = sum[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    constexpr int SB = 4;  // partials per batch of loads
-    for (int64_t p0 = 0; p0 < parts; p0 += SB) {
-      f32x4 v[SB][MT][2];
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = xg + static_cast<int64_t>(min(16 * mt + n, a.T - 1)) * a.xs + 8 * g;  // padded tokens: the last real one
+
+  struct Stage {
+    V8 wgt[2], wup[2];
+    V8 xv[MT][2];
+  };
+  Stage ring[NS];
+  auto issue = [&](Stage& st, int j) {
+    const int t = min(j, nu - 1);  // past the run: repeat its last unit
+    const int64_t kk = ((u0 + t) % nk) * kGuBK;
+    const T* up = wp + gu_packed_pos(blockIdx.x, t, total, gridDim.x) * (2 * kGuWaves * 2 * kWave * 8);
 #pragma unroll
-      for (int u = 0; u < SB; ++u) {
-        const CoherentRsrc rs = part_rsrc(sl, min<int64_t>(p0 + u, parts - 1));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int gu = 0; gu < 2; ++gu)
-            v[u][mt][gu] = p0 + u < parts ? load_coherent<4>(rs, part_off(mt, gu)) : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int u = 0; u < SB; ++u)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int gu = 0; gu < 2; ++gu) sum[mt][gu] += v[u][mt][gu];
+    for (int h = 0; h < 2; ++h) {
+      const T* f = up + h * (kGuWaves * 2 * kWave * 8);
+      st.wgt[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f));
+      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + kWave * 8));
     }
-    emit(sl, sum);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) st.xv[mt][h] = __builtin_bit_cast(V8, load_pack<T, 8>(xrow[mt] + kk + 32 * h));
+  };
+  f32x4 acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    issue(ring[d], d);
+    __builtin_amdgcn_sched_barrier(0);  // stages issued in ring order, oldest consumed first
   }
+  for (int j0 = 0; j0 < nu; j0 += NS) {
+#pragma unroll
+    for (int d = 0; d < NS; ++d) {
+      const int j = j0 + d;
+      if (j < nu) {  // uniform
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt][0] = M::run(ring[d].wgt[h], ring[d].xv[mt][h], acc[mt][0]);
+            acc[mt][1] = M::run(ring[d].wup[h], ring[d].xv[mt][h], acc[mt][1]);
+          }
+      }
+      // Every unit issues the same loads on every path (past the run, again the run's last
+      // unit, from L2), so the compiler can count how many are still in flight when a stage
+      // is consumed: NS - 1 stages. With a skipped issue on one path it waits for all.
+      issue(ring[d], j + NS);
+      __builtin_amdgcn_sched_barrier(0);
+      // Drain the slab's stores here (once per slab), for the same reason: with stores and
+      // loads both pending, the loads cannot be counted apart.
+      if (j < nu) run.template end_unit<true>(j, nu, acc);
+    }
+  }
+  run.merge(last_flags);
+}
+
+// Packs W [2I, H] (row stride ws) into the layout of k_gate_up_silu_packed for a grid of G
+// workgroups: thread t of the grid moves the 16-byte piece t of the unit-major order
+// ((((slab * nk32 + step) * 4 + wave) * 2 + part) * 64 + lane) to its unit's packed place.
+template <typename T>
+__global__ void __launch_bounds__(256) k_gu_pack(const T* __restrict__ w, int64_t ws, T* __restrict__ dst, int H,
+                                                 int I, int64_t G, int64_t pieces) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= pieces) return;
+  const int lane = static_cast<int>(t & 63);
+  int64_t r = t >> 6;
+  const int part = static_cast<int>(r & 1);
+  r >>= 1;
+  const int wave = static_cast<int>(r & 3);
+  r >>= 2;
+  const int nk32 = H / 32;
+  const int step = static_cast<int>(r % nk32);
+  const int64_t slab = r / nk32;
+  const int64_t row = part * static_cast<int64_t>(I) + slab * kGuSlab + wave * kGuRows + (lane & 15);
+  const int64_t k = static_cast<int64_t>(step) * 32 + 8 * (lane >> 4);
+  const int64_t nk = H / kGuBK, total = static_cast<int64_t>(I / kGuSlab) * nk;
+  const int64_t u = slab * nk + step / 2;
+  const int64_t b = gu_owner(u, total, G);
+  const int64_t pos = gu_packed_pos(b, u - gu_start(b, total, G), total, G);
+  const int64_t in_unit = ((((step & 1) * kGuWaves + wave) * 2 + part) * kWave + lane);
+  store_pack<T, 8>(dst + (pos * (2 * kGuWaves * 2 * kWave) + in_unit) * 8, load_pack<T, 8>(w + row * ws + k));
 }
 
 template <typename T, int MT>
@@ -356,6 +527,24 @@ int launch_gu(const GuArgs& a, int64_t programs, hipStream_t st) {
   hipLaunchKernelGGL((k_gate_up_silu<T, MT, EMBER_GU_STAGES, (MT <= EMBER_GU_PRIVX_MT)>),
                      dim3(static_cast<uint32_t>(programs)), dim3(kGuWaves * kWave), 0, st, a);
   return launch_status();
+}
+
+template <typename T, int MT>
+int launch_gu_packed(const GuArgs& a, int64_t programs, hipStream_t st) {
+  hipLaunchKernelGGL((k_gate_up_silu_packed<T, MT, EMBER_GU_PACKED_STAGES>), dim3(static_cast<uint32_t>(programs)),
+                     dim3(kGuWaves * kWave), 0, st, a);
+  return launch_status();
+}
+
+template <typename T>
+int launch_gu_packed_typed(const GuArgs& a, int64_t programs, hipStream_t st) {
+  switch ((a.T + 15) / 16) {
+    case 1: return launch_gu_packed<T, 1>(a, programs, st);
+    case 2: return launch_gu_packed<T, 2>(a, programs, st);
+    case 3: return launch_gu_packed<T, 3>(a, programs, st);
+    case 4: return launch_gu_packed<T, 4>(a, programs, st);
+    default: return EMBER_EINVAL;
+  }
 }
 
 template <typename T>
@@ -575,10 +764,15 @@ int64_t ember_gate_up_silu_workspace_bytes(int64_t tokens, int64_t hidden, int64
   return partials + (slabs * int64_t(sizeof(uint32_t)) + 255) / 256 * 256;
 }
 
-int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
-                       int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
-                       int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
-  if (tokens == 0) return EMBER_OK;
+}  // extern "C"
+
+namespace ember {
+namespace {
+
+// Validates a dense call and fills its arguments (w_row_stride is ignored for packed weights).
+int gu_setup(GuArgs& a, GuPlan& p, const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+             bool packed, int dtype, int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups,
+             void* workspace, int64_t workspace_bytes, void* out, int64_t out_row_stride) {
   if (tokens < 0 || tokens > kGuMaxTokens || hidden < kGuBK || hidden % kGuBK != 0 || inter < kGuSlab ||
       inter % kGuSlab != 0 || inter > (int64_t(1) << 29) || hidden > (int64_t(1) << 24) || num_workgroups < 1)
     return EMBER_EINVAL;
@@ -587,13 +781,12 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
       !aligned16(out) || !aligned16(workspace))
     return EMBER_EINVAL;
   // 16-byte rows and 8-byte output packs
-  if (x_row_stride < hidden || w_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 ||
-      w_row_stride % 8 != 0 || out_row_stride % 4 != 0)
+  if (x_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 || out_row_stride % 4 != 0)
     return EMBER_EINVAL;
+  if (!packed && (w_row_stride < hidden || w_row_stride % 8 != 0)) return EMBER_EINVAL;
   const int64_t need = ember_gate_up_silu_workspace_bytes(tokens, hidden, inter, num_workgroups);
   if (need < 0 || workspace_bytes < need) return EMBER_EINVAL;
-  const GuPlan p = gu_plan(hidden, inter, num_workgroups);
-  GuArgs a{};
+  p = gu_plan(hidden, inter, num_workgroups);
   a.x = x;
   a.xs = x_row_stride;
   a.w = w;
@@ -608,9 +801,61 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
   a.part = static_cast<float*>(workspace);
   a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
                                            slabs * p.max_parts * gu_partial_floats(tokens) * int64_t(sizeof(float)));
+  return EMBER_OK;
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
+                       int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
+                       int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+  if (tokens == 0) return EMBER_OK;
+  GuArgs a{};
+  GuPlan p;
+  const int rc = gu_setup(a, p, x, x_row_stride, w, w_row_stride, false, dtype, tokens, hidden, inter, num_workgroups,
+                          workspace, workspace_bytes, out, out_row_stride);
+  if (rc != EMBER_OK) return rc;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return dtype == EMBER_F16 ? launch_gu_typed<_Float16>(a, p.programs, st)
                             : launch_gu_typed<__bf16>(a, p.programs, st);
+}
+
+int ember_gate_up_silu_pack_weight(const void* w, int64_t w_row_stride, int dtype, int64_t hidden, int64_t inter,
+                                   int64_t num_workgroups, void* packed, void* stream) {
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (num_workgroups < 1) return EMBER_EINVAL;
+  if (hidden < kGuBK || hidden % kGuBK != 0 || inter < kGuSlab || inter % kGuSlab != 0 ||
+      inter > (int64_t(1) << 29) || hidden > (int64_t(1) << 24) || w_row_stride < hidden || w_row_stride % 8 != 0)
+    return EMBER_EINVAL;
+  if (w == nullptr || packed == nullptr || !aligned16(w) || !aligned16(packed)) return EMBER_EINVAL;
+  const int64_t G = gu_plan(hidden, inter, num_workgroups).programs;  // as the kernel's grid
+  const int64_t pieces = 2 * inter * hidden / 8;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(cdiv(pieces, 256)));
+  if (dtype == EMBER_F16)
+    hipLaunchKernelGGL(k_gu_pack<_Float16>, grid, dim3(256), 0, st, static_cast<const _Float16*>(w), w_row_stride,
+                       static_cast<_Float16*>(packed), static_cast<int>(hidden), static_cast<int>(inter), G, pieces);
+  else
+    hipLaunchKernelGGL(k_gu_pack<__bf16>, grid, dim3(256), 0, st, static_cast<const __bf16*>(w), w_row_stride,
+                       static_cast<__bf16*>(packed), static_cast<int>(hidden), static_cast<int>(inter), G, pieces);
+  return launch_status();
+}
+
+int ember_gate_up_silu_packed(const void* x, int64_t x_row_stride, const void* packed_w, int dtype, int64_t tokens,
+                              int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
+                              int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+  if (tokens == 0) return EMBER_OK;
+  GuArgs a{};
+  GuPlan p;
+  const int rc = gu_setup(a, p, x, x_row_stride, packed_w, 0, true, dtype, tokens, hidden, inter, num_workgroups,
+                          workspace, workspace_bytes, out, out_row_stride);
+  if (rc != EMBER_OK) return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return dtype == EMBER_F16 ? launch_gu_packed_typed<_Float16>(a, p.programs, st)
+                            : launch_gu_packed_typed<__bf16>(a, p.programs, st);
 }
 
 int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter, int64_t num_blocks,

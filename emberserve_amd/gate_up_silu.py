@@ -74,9 +74,50 @@ def _fits(x2: Tensor, weight: Tensor, out: Tensor) -> bool:
             and x2.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0)
 
 
+class PackedGateUp:
+    """A gate_up weight [2I, H] rearranged for `ember_gate_up_silu_packed` run with
+    `num_workgroups` workgroups: every MFMA operand fragment of the decode kernel is one
+    contiguous KiB, and the units of work sit in the order the grid reads them, so the whole
+    grid streams the weights front to back. Made once per weight by `pack_gate_up_weight`;
+    holds 2 I H elements (the same bytes as the weight, which the caller keeps for the
+    unfused path above FUSED_TOKENS)."""
+
+    def __init__(self, packed: Tensor, hidden: int, inter: int, num_workgroups: int) -> None:
+        self.packed, self.hidden, self.inter, self.num_workgroups = packed, hidden, inter, num_workgroups
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.packed.dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.packed.device
+
+
+def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> PackedGateUp:
+    """The packed copy of weight [2I, H] (fp16/bf16 on the GPU, H and I multiples of 64) for
+    a grid of `num_workgroups` (default: one per CU, the decode kernel's default)."""
+    if weight.dim() != 2 or weight.shape[0] % 2 != 0 or weight.dtype not in SUPPORTED_DTYPES:
+        raise ValueError(f"pack_gate_up_weight: a [2I, H] fp16/bf16 weight expected, got {tuple(weight.shape)} "
+                         f"{weight.dtype}")
+    _require_device("pack_gate_up_weight", weight)
+    two_i, H = weight.shape
+    I = two_i // 2
+    if H % STEP or I % SLAB or weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
+        raise ValueError("pack_gate_up_weight: H and I must be multiples of 64, rows unit-stride and 16-byte aligned")
+    programs = gate_up_silu_workgroups(weight.device) if num_workgroups is None else int(num_workgroups)
+    if programs < 1:
+        raise ValueError(f"pack_gate_up_weight: num_workgroups must be >= 1, got {programs}")
+    packed = torch.empty(two_i * H, dtype=weight.dtype, device=weight.device)
+    _launch("ember_gate_up_silu_pack_weight", _lib.load().ember_gate_up_silu_pack_weight, weight.device,
+            weight.data_ptr(), weight.stride(0), _lib.dtype_tag(weight.dtype), H, I, programs, packed.data_ptr())
+    return PackedGateUp(packed, H, I, programs)
+
+
 def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None,
-                 fused: bool | None = None) -> Tensor:
-    """silu_and_mul(F.linear(x, weight)) with weight [2I, H] (qwen2.py:60-61)."""
+                 fused: bool | None = None, packed: PackedGateUp | None = None) -> Tensor:
+    """silu_and_mul(F.linear(x, weight)) with weight [2I, H] (qwen2.py:60-61). With `packed`
+    (`pack_gate_up_weight(weight)`), the fused kernel reads the packed copy instead."""
     if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
         raise ValueError(f"gate_up_silu: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
                          "a [2I, H] gate_up projection")
@@ -93,13 +134,25 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     if fused is False or (fused is None and T > FUSED_TOKENS) or not _fits(x2, weight, out):
         return gate_up_silu_torch(x, weight)
     programs = gate_up_silu_workgroups(x.device) if num_workgroups is None else int(num_workgroups)
+    if packed is not None:
+        if num_workgroups is not None and programs != packed.num_workgroups:
+            raise ValueError(f"gate_up_silu: the weight was packed for {packed.num_workgroups} workgroups, "
+                             f"not {programs}")
+        programs = packed.num_workgroups
     if programs < 1:
         raise ValueError(f"gate_up_silu: num_workgroups must be >= 1, got {programs}")
     tiles = -(-T // 16)
     ws = _SCRATCH.get((programs, tiles, H, I), lambda: _workspace_bytes(programs, tiles, H, I), x.device)
-    _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
-            x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
-            T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+    if packed is not None:
+        if (packed.hidden, packed.inter, packed.dtype, packed.device) != (H, I, x.dtype, x.device):
+            raise ValueError("gate_up_silu: the packed weight does not match x and weight")
+        _launch("ember_gate_up_silu_packed", _lib.load().ember_gate_up_silu_packed, x.device,
+                x2.data_ptr(), x2.stride(0), packed.packed.data_ptr(), _lib.dtype_tag(x.dtype),
+                T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+    else:
+        _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
+                x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
+                T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
     if _check_indices():
         need, slabs = _workspace_bytes(programs, tiles, H, I), I // SLAB
         _SCRATCH.verify_counters(ws, need - round_up(slabs * 4, 256), need - round_up(slabs * 4, 256) + slabs * 4)

@@ -397,6 +397,30 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
                            int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
                            int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
 
+/* Rearranges a gate_up weight W [2I, H] (row stride w_row_stride elements, fp16 or bf16,
+ * 16-byte aligned) into the layout ember_gate_up_silu_packed reads with num_workgroups
+ * workgroups: 2 I H elements in units of 8192. Unit (slab, j) (slab < I / 64, j < H / 64) is
+ *   unit[h][wave][part][lane][8] = W[part I + 64 slab + 16 wave + lane % 16]
+ *                                   [64 j + 32 h + 8 (lane / 16) + 0..7]
+ * (h < 2, wave < 4, part 0 gate / 1 up, lane < 64). With U = (I / 64)(H / 64) units and
+ * G = min(num_workgroups, U), workgroup b owns units [floor(b U / G), floor((b + 1) U / G))
+ * in slab-major order; its t-th unit is stored at unit position t G + b while t < U / G
+ * (integer division), and the extra unit of a longer run after all of those, in workgroup
+ * order. A pure permutation, done once per weight (at load time); H and I multiples of 64.
+ * No counterpart in the reference: the layout is this library's, chosen so that the decode
+ * kernel's grid reads the weights front to back. */
+int ember_gate_up_silu_pack_weight(const void* w, int64_t w_row_stride, int dtype, int64_t hidden, int64_t inter,
+                                   int64_t num_workgroups, void* packed, void* stream);
+
+/* ember_gate_up_silu over a weight packed by ember_gate_up_silu_pack_weight: the same
+ * results (bit-identical: the same products in the same order), the same workspace
+ * (ember_gate_up_silu_workspace_bytes) and limits; replaces the same reference call
+ * (qwen2.py:60-61). num_workgroups must be the value the weight was packed for (the
+ * library cannot check it: another value reads the wrong units). */
+int ember_gate_up_silu_packed(const void* x, int64_t x_row_stride, const void* packed_w, int dtype, int64_t tokens,
+                              int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
+                              int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+
 /* Bytes of workspace ember_moe_gate_up_silu needs for num_splits > 1 (0 for one split), -1
  * for invalid arguments: fp32 partials [num_splits][num_valid][2 inter] and one uint32
  * arrival counter per (block, 64-column slab). */

@@ -43,6 +43,7 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
   moe_gate_up_silu             every token routed to one expert equals gate_up_silu with
                                that expert's weight, row by row; rows follow the assignment
                                order t * k + c; experts are picked by index, not position.
+  pack_gate_up_weight          an element-by-element index definition on a small weight.
   moe_align                    the reference's own layout case (tests/test_moe_triton.py:
                                34-48) written out slot by slot; every assignment exactly once;
                                runs ascending and block-aligned; sizes; all-one-expert and
@@ -106,6 +107,24 @@ def gate_up_silu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     the activation's is the one to the dtype."""
     gate_up = (x.double() @ weight.double().T).to(x.dtype)
     return silu_and_mul(gate_up)
+
+
+def pack_gate_up_weight(weight: torch.Tensor, num_workgroups: int) -> torch.Tensor:
+    """The packed gate_up weight layout of this library's decode kernel for a grid of
+    num_workgroups (no counterpart in the reference; a permutation of W [2I, H]). Units
+    (slab, j) of 8192 elements, unit[h][wave][part][lane][8] = W[part I + 64 slab + 16 wave +
+    lane % 16][64 j + 32 h + 8 (lane // 16) + e]; workgroup b runs units [b U // G, (b + 1) U
+    // G) of the slab-major order, and the packed array lists the runs' units round by round:
+    the first unit of every run in workgroup order, then the second, and so on."""
+    two_i, h = weight.shape
+    i = two_i // 2
+    v = weight.reshape(2, i // 64, 4, 16, h // 64, 2, 4, 8)   # part, slab, wave, n, j, h, g, e
+    units = v.permute(1, 4, 5, 2, 0, 6, 3, 7).reshape(-1, 8192)  # slab, j, h, wave, part, g, n, e
+    total = units.shape[0]
+    g = min(num_workgroups, total)
+    runs = [list(range(b * total // g, (b + 1) * total // g)) for b in range(g)]
+    order = [run[t] for t in range(max(len(r) for r in runs)) for run in runs if t < len(run)]
+    return units[torch.tensor(order)].reshape(-1)
 
 
 def moe_gate_up_silu(x: torch.Tensor, topk_ids: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:

@@ -158,3 +158,57 @@ def test_swiglu_mlp_module_on_the_gpu():
         got = mlp(x)
         want = mlp.down_proj(gate_up_silu(x, mlp.gate_up_proj.weight))
     assert torch.equal(got, want)
+
+
+# ---- the packed weight layout (ember_gate_up_silu_pack_weight / ember_gate_up_silu_packed) ----
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("programs", [1, 7, 256, 5000])
+def test_pack_weight_matches_the_oracle_permutation(dtype, programs):
+    """H 192, I 320: 15 units, so 7 workgroups give runs of 2 and 3 units and 256 or 5000
+    clamp to 15."""
+    from emberserve_amd.gate_up_silu import pack_gate_up_weight
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(2 * 320, 192, generator=g).to(dtype)
+    packed = pack_gate_up_weight(w.to(DEV), programs)
+    assert torch.equal(packed.packed.cpu().view(torch.int16), ref.pack_gate_up_weight(w, programs).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens", [1, 7, 16, 33, 64])
+@pytest.mark.parametrize("programs", [7, 256, 300])
+def test_packed_kernel_equals_the_row_kernel(dtype, tokens, programs):
+    """Same products in the same order: bit-identical to ember_gate_up_silu (Qwen2.5-0.5B
+    MLP, H 896, I 4864), including runs that split slabs and merge partials."""
+    from emberserve_amd.gate_up_silu import pack_gate_up_weight
+    _say(f"packed gate_up {dtype} T={tokens} G={programs}")
+    g = torch.Generator().manual_seed(tokens)
+    x = (torch.randn(tokens, 896, generator=g) * 0.5).to(dtype).to(DEV)
+    w = (torch.randn(2 * 4864, 896, generator=g) / 896 ** 0.5).to(dtype).to(DEV)
+    packed = pack_gate_up_weight(w, programs)
+    a = gate_up_silu(x, w, num_workgroups=programs, fused=True)
+    b = gate_up_silu(x, w, fused=True, packed=packed)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_packed_kernel_qwen3_8b_against_oracle(tokens):
+    """Qwen3-8B MLP (H 4096, I 12288) bf16 on sampled output columns against the oracle."""
+    from emberserve_amd.gate_up_silu import pack_gate_up_weight
+    _say(f"packed gate_up qwen3-8b T={tokens}")
+    g = torch.Generator().manual_seed(40 + tokens)
+    x = (torch.randn(tokens, 4096, generator=g) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(2 * 12288, 4096, generator=g) / 64).to(torch.bfloat16)
+    wd = w.to(DEV)
+    got = gate_up_silu(x.to(DEV), wd, fused=True, packed=pack_gate_up_weight(wd)).cpu()
+    cols = torch.randperm(12288, generator=g)[:512]
+    ws = torch.cat([w[cols], w[12288 + cols]])
+    _check(got[:, cols], x, ws, "packed qwen3-8b")
+
+
+def test_packed_weight_rejects_another_grid():
+    from emberserve_amd.gate_up_silu import pack_gate_up_weight
+    w = torch.randn(2 * 128, 64, device=DEV).to(torch.bfloat16)
+    x = torch.randn(1, 64, device=DEV).to(torch.bfloat16)
+    packed = pack_gate_up_weight(w, 3)
+    with pytest.raises(ValueError, match="packed for 3"):
+        gate_up_silu(x, w, num_workgroups=4, fused=True, packed=packed)

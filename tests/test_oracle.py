@@ -647,3 +647,34 @@ def test_moe_align_oracle_properties(n, e, k, bm):
             assert not rows
         else:
             assert rows == sorted(rows) and all(flat[v] == x for v in rows)
+
+
+@pytest.mark.parametrize("groups", [1, 3, 4, 7, 100])
+def test_pack_gate_up_weight_index_definition(groups):
+    """Element by element against the layout's closed form: unit (slab, j) of U units holds
+    W[part I + 64 slab + 16 wave + lane % 16][64 j + 32 h + 8 (lane // 16) + e] at
+    ((h * 4 + wave) * 2 + part) * 64 + lane, and the t-th unit of workgroup b's run is stored at
+    t G + b while t < U // G, the extra units of longer runs after those in workgroup order
+    (G = min(groups, U); runs of 3 and 4 units at G 7, a clamp at 100)."""
+    i, h = 128, 128
+    w = torch.arange(2 * i * h, dtype=torch.float64).view(2 * i, h)
+    p = ref.pack_gate_up_weight(w, groups)
+    assert p.numel() == w.numel()
+    total = (i // 64) * (h // 64)
+    g = min(groups, total)
+    q = total // g
+    pos = {}
+    for b in range(g):
+        start = b * total // g
+        for t in range((b + 1) * total // g - start):
+            pos[start + t] = t * g + b if t < q else q * g + (start - b * q)
+    assert sorted(pos.values()) == list(range(total))
+    for slab in range(i // 64):
+        for j in range(h // 64):
+            base = pos[slab * (h // 64) + j] * 8192
+            for idx in range(0, 8192, 29):
+                e, lane, part, wave, hh = idx % 8, idx // 8 % 64, idx // 512 % 2, idx // 1024 % 4, idx // 4096
+                row = part * i + 64 * slab + 16 * wave + lane % 16
+                col = 64 * j + 32 * hh + 8 * (lane // 16) + e
+                assert float(p[base + idx]) == float(w[row, col]), (groups, slab, j, idx)
+    assert sorted(p.tolist()) == list(range(w.numel()))  # a permutation
