@@ -386,24 +386,34 @@ def _ops(torch, ops, tables):
         """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's
         geometry (H 2048, I 1408, 64 experts, top-6), decode batch n: bytes are the used
         experts' weights (each read once) plus x and the activations."""
-        from emberserve_amd.moe import moe_align, moe_gate_up_silu
+        from emberserve_amd.moe import moe_align, moe_gate_up_silu, pack_moe_gate_up_weight
         h, inter, ne, k = 2048, 1408, 64, 6
         g.manual_seed(290 + n)
         ids = torch.stack([torch.randperm(ne, generator=g, device=dev)[:k] for _ in range(n)])
-        used = int(torch.unique(ids).numel())
+        used_ids = torch.unique(ids)
+        used = int(used_ids.numel())
         sorted_ids, block_expert, nv = moe_align(ids, ne)
 
-        def make(i):
-            return (randn((n, h), bf, 300 + i, std=0.5), randn((ne, 2 * inter, h), bf, 310 + i, std=h ** -0.5))
+        def make(i):  # only the used experts' weights are read, so only they are filled
+            w = torch.empty((ne, 2 * inter, h), dtype=bf, device=dev)
+            w[used_ids] = randn((used, 2 * inter, h), bf, 310 + i, std=h ** -0.5)
+            return randn((n, h), bf, 300 + i, std=0.5), w
+        # input sets rotate over the bytes a launch touches (the used experts), so a launch
+        # never finds its weights in the Infinity Cache
         wbytes = used * 2 * inter * h * 2
         nbytes = wbytes + n * h * 2 + n * k * inter * 2
         out.append(Op("moe_gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts ({used} used), "
                       f"w[{ne},{2 * inter},{h}] bf16", nbytes, make,
-                      lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k), ne * 2 * inter * h * 2))
+                      lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k), wbytes))
+        def make_packed(i):  # the experts packed once, at load time, outside the timed region
+            x, w = make(i)
+            return x, w, pack_moe_gate_up_weight(w)
+        out.append(Op("moe_gate_up_silu_packed", cfg, f"moonlight: N={n} top-{k} of {ne} experts ({used} used), "
+                      f"w[{ne},{2 * inter},{h}] bf16 packed at load", nbytes, make_packed,
+                      lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k, packed=a[2]), wbytes))
         # the same with the alignment launched each time (ember_moe_align + the grouped kernel)
         out.append(Op("moe_align+gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts, align each call",
-                      nbytes, make, lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k),
-                      ne * 2 * inter * h * 2))
+                      nbytes, make, lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes))
 
     def moe_align_row(cfg, n, ne=64, k=6):
         """ember_moe_align alone (moe_triton.py:215-254's layout in one launch): bytes are the

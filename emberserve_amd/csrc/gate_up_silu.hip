@@ -53,6 +53,10 @@
 // Token tiles (of 16) up to which every wave loads its own copy of x. Measured on MI355X
 // (persistent grid, one workgroup per CU): private and shared copies tie at 1-16 tokens;
 // at 32 tokens the shared copy is faster (Qwen3-8B 41.2 vs 41.9 us, Qwen2.5-7B 59.2 vs 61.4).
+// Register ring stages of the packed routed-expert kernel.
+#ifndef EMBER_MOE_PACKED_STAGES
+#define EMBER_MOE_PACKED_STAGES 3
+#endif
 #ifndef EMBER_GU_PRIVX_MT
 #define EMBER_GU_PRIVX_MT 1
 #endif
@@ -446,14 +450,16 @@ k_gate_up_silu_packed(GuArgs a) {
   };
   Stage ring[NS];
   auto issue = [&](Stage& st, int j) {
-    const int t = min(j, nu - 1);  // past the run: repeat its last unit
+    const int t = min(j, nu - 1);
     const int64_t kk = ((u0 + t) % nk) * kGuBK;
+    // past the run: repeat its last unit (measured: as fast as reading x there instead)
     const T* up = wp + gu_packed_pos(blockIdx.x, t, total, gridDim.x) * (2 * kGuWaves * 2 * kWave * 8);
+    constexpr int hs = kGuWaves * 2 * kWave * 8, ps = kWave * 8;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const T* f = up + h * (kGuWaves * 2 * kWave * 8);
+      const T* f = up + h * hs;
       st.wgt[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f));
-      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + kWave * 8));
+      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + ps));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -596,6 +602,9 @@ GuPlan gu_plan(int64_t hidden, int64_t inter, int64_t programs) {
 // (small batches, where blocks x slabs alone leave CUs idle) each split stores fp32
 // partials at its rows' assignment ids, and the last split of a (block, slab) to arrive
 // sums them in k order.
+// Blocks per call: the grid's third dimension (1M assignments in 16-row blocks).
+constexpr int64_t kMoeMaxBlocks = 65535;
+
 struct MoeGuArgs {
   const void* x;
   int64_t xs, ntok;
@@ -606,11 +615,88 @@ struct MoeGuArgs {
   const int32_t* sorted_ids;
   const int32_t* block_expert;
   int E, H, I, num_valid, a_div;
-  int kc;             // k per split (gridDim.z splits)
+  int kc;             // k per split
   float* part;        // [splits][num_valid][2I] fp32 partials (splits > 1)
   uint32_t* counters; // [num_blocks][I / 64] arrival counters (splits > 1)
   uint32_t* err;
 };
+
+// The end of a routed-expert workgroup (block blk, slab): with k splits, leave this split's
+// fp32 partials, and the last split of (blk, slab) to arrive sums them in k order; then the
+// silu_and_mul epilogue at the block's assignment rows. Shared by both weight layouts.
+// A routed-expert workgroup's (block, slab, k split). The grid is (slabs, splits, blocks):
+// the workgroups of one block dispatch together, and the used blocks (the layout's first)
+// before the empty ones, which exit at once. Measured on MI355X at one token (6 of 60
+// blocks used): the packed kernel takes 24 us with the block index fastest (its working
+// workgroups then land on few CUs) and 15 us this way; the row kernel 17 and 12.7 us.
+struct MoeTile {
+  int blk, slab, split, splits;
+};
+__device__ __forceinline__ MoeTile moe_tile() {
+  return MoeTile{static_cast<int>(blockIdx.z), static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y),
+                 static_cast<int>(gridDim.y)};
+}
+
+template <typename T>
+__device__ __forceinline__ void moe_finish(const MoeGuArgs& a, f32x4 (&acc)[2], const MoeTile& tile, int w,
+                                           int lane) {
+  const int blk = tile.blk, slab = tile.slab;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  // lane (n, g): assignment n of the block, output columns slab * 64 + 16 w + 4g + [0, 4)
+  const int id = a.sorted_ids[blk * 16 + n];
+  const bool mine = id >= 0 && id < a.num_valid;
+  const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
+  const int splits = tile.splits;
+  if (splits > 1) {
+    const int64_t row_floats = 2 * static_cast<int64_t>(a.I);
+    const int part_floats = static_cast<int>(splits * a.num_valid * row_floats);
+    const CoherentRsrc rs = coherent_rsrc(a.part, part_floats);
+    const int off = static_cast<int>(((tile.split * static_cast<int64_t>(a.num_valid) + (mine ? id : 0)) * row_floats + col) * 4);
+    if (mine) {
+      store_coherent<4>(rs, off, acc[0]);
+      store_coherent<4>(rs, off + a.I * 4, acc[1]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ int is_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t* cnt = a.counters + static_cast<int64_t>(blk) * (a.I / kGuSlab) + slab;
+      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = prev == static_cast<uint32_t>(splits - 1);
+      if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last || !mine) return;
+    // the splits in k order, all loads in flight together (at most 4 splits)
+    f32x4 v[4][2];
+    const int row0 = static_cast<int>((static_cast<int64_t>(id) * row_floats + col) * 4);
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp) {
+      const int o = static_cast<int>(min(sp, splits - 1) * static_cast<int64_t>(a.num_valid) * row_floats * 4) + row0;
+      v[sp][0] = load_coherent<4>(rs, o);
+      v[sp][1] = load_coherent<4>(rs, o + a.I * 4);
+    }
+    acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < 4; ++sp)
+      if (sp < splits) {
+        acc[0] += v[sp][0];
+        acc[1] += v[sp][1];
+      }
+  }
+  if (mine) {
+    Pack<T, 4> o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gf = round_to<T>(acc[0][i]);
+      const float uf = round_to<T>(acc[1][i]);
+      const float act = round_to<T>(gf / (1.0f + expf(-gf)));
+      o.v[i] = from_f32<T>(act * uf);
+    }
+    store_pack<T, 4>(static_cast<T*>(a.out) + static_cast<int64_t>(id) * a.os + col, o);
+  }
+}
 
 template <typename T, int NS>
 __global__ void __launch_bounds__(kGuWaves * kWave, 1)
@@ -625,16 +711,17 @@ k_moe_gate_up_silu(MoeGuArgs a) {
   static_assert(NS >= 2 && NS <= 4, "stages");
   __shared__ __attribute__((aligned(16))) unsigned char lds[NS * STAGE];
 
-  const int blk = blockIdx.x;
+  const MoeTile tile = moe_tile();
+  const int blk = tile.blk;
   const int e = a.block_expert[blk];  // uniform (scalar load)
   if (e < 0 || e >= a.E) return;
-  const int slab = blockIdx.y;
+  const int slab = tile.slab;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
   const int nk = a.kc / kGuBK;
-  const int k0 = blockIdx.z * a.kc;
+  const int k0 = tile.split * a.kc;
   const int lr = lane >> 3;
   const int lc = (lane & 7) ^ lr;
 
@@ -691,59 +778,114 @@ k_moe_gate_up_silu(MoeGuArgs a) {
     if (j + NS - 1 < nk) issue(j + NS - 1);
     compute(j);
   }
-  // lane (n, g): assignment n of the block, output columns slab * 64 + 16 w + 4g + [0, 4)
+  moe_finish<T>(a, acc, tile, w, lane);
+}
+
+
+// The packed form of the routed experts' kernel: each expert's weights pre-arranged once
+// (ember_moe_gate_up_silu_pack_weight) in the dense packed kernel's 16 KiB units, ordered
+// k-major: expert e, unit (j, slab) at e * 2 I H + (j * I / 64 + slab) * 8192 elements. The
+// workgroups of one expert and k split then read one window of I / 64 adjacent units at a
+// time, each load instruction moves 1 KiB of consecutive lanes, and the ring is in registers,
+// so no LDS limits how many workgroups share a CU. Same grid, products, order and epilogue
+// as k_moe_gate_up_silu: bit-identical results.
+template <typename T, int NS>
+__global__ void __launch_bounds__(kGuWaves * kWave)
+k_moe_gate_up_silu_packed(MoeGuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  static_assert(NS >= 2 && NS <= 8, "stages");
+  const MoeTile tile = moe_tile();
+  const int blk = tile.blk;
+  const int e = a.block_expert[blk];  // uniform (scalar load)
+  if (e < 0 || e >= a.E) return;
+  const int slab = tile.slab;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int nk = a.kc / kGuBK;
+  const int slabs = a.I / kGuSlab;
+  constexpr int kUnit = 2 * kGuWaves * 2 * kWave * 8;  // elements
+  const T* wp = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes +
+                (static_cast<int64_t>(tile.split) * nk * slabs + slab) * kUnit + (w * 2 * kWave + lane) * 8;
+  const int64_t ustride = static_cast<int64_t>(slabs) * kUnit;
   const int id = a.sorted_ids[blk * 16 + n];
-  const bool mine = id >= 0 && id < a.num_valid;
-  const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
-  const int splits = gridDim.z;
-  if (splits > 1) {
-    const int64_t row_floats = 2 * static_cast<int64_t>(a.I);
-    const int part_floats = static_cast<int>(splits * a.num_valid * row_floats);
-    const CoherentRsrc rs = coherent_rsrc(a.part, part_floats);
-    const int off = static_cast<int>(((blockIdx.z * static_cast<int64_t>(a.num_valid) + (mine ? id : 0)) * row_floats + col) * 4);
-    if (mine) {
-      store_coherent<4>(rs, off, acc[0]);
-      store_coherent<4>(rs, off + a.I * 4, acc[1]);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __shared__ int is_last;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t* cnt = a.counters + static_cast<int64_t>(blk) * gridDim.y + slab;
-      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      is_last = prev == static_cast<uint32_t>(splits - 1);
-      if (is_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!is_last || !mine) return;
-    // the splits in k order, all loads in flight together (at most 4 splits)
-    f32x4 v[4][2];
-    const int row0 = static_cast<int>((static_cast<int64_t>(id) * row_floats + col) * 4);
+  int64_t row = id >= 0 && id < a.num_valid ? id / a.a_div : 0;
+  if (row >= a.ntok) {
+    atomicOr(a.err, EMBER_ERR_ROW_INDEX);
+    row = 0;
+  }
+  const T* xrow = static_cast<const T*>(a.x) + row * a.xs + static_cast<int64_t>(tile.split) * a.kc + 8 * g;
+
+  struct Stage {
+    V8 wgt[2], wup[2], xv[2];
+  };
+  Stage ring[NS];
+  auto issue = [&](Stage& st, int j) {
+    const int jj = min(j, nk - 1);
+    // past the range: the same instructions on this lane's x row (L2), not more weights.
+    // Measured: 0.3-1 us faster than re-reading the range's last unit at 1-4 tokens.
+    const bool real = j < nk;
+    const T* f = real ? wp + jj * ustride : xrow;
+    const int hs = real ? kGuWaves * 2 * kWave * 8 : 0, ps = real ? kWave * 8 : 0;
 #pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-      const int o = static_cast<int>(min(sp, splits - 1) * static_cast<int64_t>(a.num_valid) * row_floats * 4) + row0;
-      v[sp][0] = load_coherent<4>(rs, o);
-      v[sp][1] = load_coherent<4>(rs, o + a.I * 4);
+    for (int h = 0; h < 2; ++h) {
+      st.wgt[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + h * hs));
+      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + h * hs + ps));
     }
-    acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int sp = 0; sp < 4; ++sp)
-      if (sp < splits) {
-        acc[0] += v[sp][0];
-        acc[1] += v[sp][1];
+    for (int h = 0; h < 2; ++h) st.xv[h] = __builtin_bit_cast(V8, load_pack<T, 8>(xrow + jj * kGuBK + 32 * h));
+  };
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    issue(ring[d], d);
+    __builtin_amdgcn_sched_barrier(0);  // stages issued in ring order, oldest consumed first
+  }
+  for (int j0 = 0; j0 < nk; j0 += NS) {
+#pragma unroll
+    for (int d = 0; d < NS; ++d) {
+      if (j0 + d < nk) {  // uniform
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[0] = M::run(ring[d].wgt[h], ring[d].xv[h], acc[0]);
+          acc[1] = M::run(ring[d].wup[h], ring[d].xv[h], acc[1]);
+        }
       }
-  }
-  if (mine) {
-    Pack<T, 4> o;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float gf = round_to<T>(acc[0][i]);
-      const float uf = round_to<T>(acc[1][i]);
-      const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-      o.v[i] = from_f32<T>(act * uf);
+      // the same loads on every path, so the compiler counts NS - 1 stages in flight
+      issue(ring[d], j0 + d + NS);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    store_pack<T, 4>(static_cast<T*>(a.out) + static_cast<int64_t>(id) * a.os + col, o);
   }
+  moe_finish<T>(a, acc, tile, w, lane);
+}
+
+// Packs the routed experts' W [E, 2I, H] (strides wes, ws) into k_moe_gate_up_silu_packed's
+// layout: thread t of the grid moves the 16-byte piece t of the source order
+// (((((e * I / 64 + slab) * H / 32 + step) * 4 + wave) * 2 + part) * 64 + lane).
+template <typename T>
+__global__ void __launch_bounds__(256) k_moe_gu_pack(const T* __restrict__ w, int64_t wes, int64_t ws,
+                                                     T* __restrict__ dst, int H, int I, int64_t pieces) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= pieces) return;
+  const int lane = static_cast<int>(t & 63);
+  int64_t r = t >> 6;
+  const int part = static_cast<int>(r & 1);
+  r >>= 1;
+  const int wave = static_cast<int>(r & 3);
+  r >>= 2;
+  const int nk32 = H / 32, slabs = I / kGuSlab;
+  const int step = static_cast<int>(r % nk32);
+  r /= nk32;
+  const int slab = static_cast<int>(r % slabs);
+  const int64_t e = r / slabs;
+  const int64_t row = part * static_cast<int64_t>(I) + slab * kGuSlab + wave * kGuRows + (lane & 15);
+  const int64_t k = static_cast<int64_t>(step) * 32 + 8 * (lane >> 4);
+  const int64_t in_unit = ((((step & 1) * kGuWaves + wave) * 2 + part) * kWave + lane);
+  const int64_t unit = static_cast<int64_t>(step / 2) * slabs + slab;
+  store_pack<T, 8>(dst + e * (2 * static_cast<int64_t>(I) * H) + (unit * (2 * kGuWaves * 2 * kWave) + in_unit) * 8,
+                   load_pack<T, 8>(w + e * wes + row * ws + k));
 }
 
 }  // namespace
@@ -869,15 +1011,25 @@ int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter,
   return (part + 255) / 256 * 256 + (num_blocks * (inter / kGuSlab) * int64_t(sizeof(uint32_t)) + 255) / 256 * 256;
 }
 
-int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
-                           int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
-                           int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
-                           int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
-                           int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
-  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+}  // extern "C"
+
+namespace ember {
+namespace {
+
+dim3 moe_grid(int64_t num_blocks, int64_t inter, int64_t num_splits) {
+  return dim3(static_cast<uint32_t>(inter / kGuSlab), static_cast<uint32_t>(num_splits),
+              static_cast<uint32_t>(num_blocks));
+}
+
+// Validates a routed-expert call and fills its arguments (strides ignored for packed weights).
+int moe_setup(MoeGuArgs& a, const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+              int64_t w_expert_stride, int64_t w_row_stride, bool packed, int dtype, int64_t num_experts,
+              int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
+              int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace, int64_t workspace_bytes, void* out,
+              int64_t out_row_stride) {
   if (num_splits < 1 || num_splits > 4 || (hidden / kGuBK) % num_splits != 0 || hidden / kGuBK / num_splits < 2)
     return EMBER_EINVAL;
-  if (num_blocks < 0 || num_blocks > 0x7fffffffLL || num_valid < 0 || num_valid > 0x7fffffffLL || top_k < 1 ||
+  if (num_blocks < 0 || num_blocks > kMoeMaxBlocks || num_valid < 0 || num_valid > 0x7fffffffLL || top_k < 1 ||
       num_tokens < 1 || num_experts < 1 || num_experts > 0x7fffffffLL || hidden < kGuBK || hidden % kGuBK != 0 ||
       hidden > (int64_t(1) << 24) || inter < kGuSlab || inter % kGuSlab != 0 || inter > (int64_t(1) << 29))
     return EMBER_EINVAL;
@@ -885,11 +1037,15 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
   if (x == nullptr || w == nullptr || out == nullptr || sorted_ids == nullptr || block_expert == nullptr ||
       !aligned16(x) || !aligned16(w) || !aligned16(out))
     return EMBER_EINVAL;
-  if (x_row_stride < hidden || w_row_stride < hidden || w_expert_stride < 2 * inter * w_row_stride ||
-      out_row_stride < inter || x_row_stride % 8 != 0 || w_row_stride % 8 != 0 || w_expert_stride % 8 != 0 ||
-      out_row_stride % 4 != 0)
+  if (x_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 || out_row_stride % 4 != 0)
     return EMBER_EINVAL;
-  MoeGuArgs a{};
+  if (packed) {
+    w_row_stride = hidden;
+    w_expert_stride = 2 * inter * hidden;
+  } else if (w_row_stride < hidden || w_expert_stride < 2 * inter * w_row_stride || w_row_stride % 8 != 0 ||
+             w_expert_stride % 8 != 0) {
+    return EMBER_EINVAL;
+  }
   a.x = x;
   a.xs = x_row_stride;
   a.ntok = num_tokens;
@@ -914,13 +1070,78 @@ int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_toke
     a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + (part + 255) / 256 * 256);
   }
   a.err = device_error_word();
-  const dim3 grid(static_cast<uint32_t>(num_blocks), static_cast<uint32_t>(inter / kGuSlab),
-                  static_cast<uint32_t>(num_splits));
+  return EMBER_OK;
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" {
+
+int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+                           int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
+                           int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
+                           int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
+                           int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  MoeGuArgs a{};
+  const int rc = moe_setup(a, x, x_row_stride, num_tokens, w, w_expert_stride, w_row_stride, false, dtype, num_experts,
+                           hidden, inter, sorted_ids, block_expert, num_blocks, num_valid, top_k, num_splits, workspace,
+                           workspace_bytes, out, out_row_stride);
+  if (rc != EMBER_OK) return rc;
+  const dim3 grid = moe_grid(num_blocks, inter, num_splits);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16) {
     hipLaunchKernelGGL((k_moe_gate_up_silu<_Float16, EMBER_MOE_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
   } else {
     hipLaunchKernelGGL((k_moe_gate_up_silu<__bf16, EMBER_MOE_STAGES>), grid, dim3(kGuWaves * kWave), 0, st, a);
+  }
+  return launch_status();
+}
+
+int ember_moe_gate_up_silu_pack_weight(const void* w, int64_t w_expert_stride, int64_t w_row_stride, int dtype,
+                                       int64_t num_experts, int64_t hidden, int64_t inter, void* packed,
+                                       void* stream) {
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (num_experts < 1 || num_experts > 0x7fffffffLL || hidden < kGuBK || hidden % kGuBK != 0 ||
+      hidden > (int64_t(1) << 24) || inter < kGuSlab || inter % kGuSlab != 0 || inter > (int64_t(1) << 29) ||
+      w_row_stride < hidden || w_expert_stride < 2 * inter * w_row_stride || w_row_stride % 8 != 0 ||
+      w_expert_stride % 8 != 0)
+    return EMBER_EINVAL;
+  if (w == nullptr || packed == nullptr || !aligned16(w) || !aligned16(packed)) return EMBER_EINVAL;
+  const int64_t pieces = num_experts * 2 * inter * hidden / 8;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(cdiv(pieces, 256)));
+  if (dtype == EMBER_F16)
+    hipLaunchKernelGGL(k_moe_gu_pack<_Float16>, grid, dim3(256), 0, st, static_cast<const _Float16*>(w),
+                       w_expert_stride, w_row_stride, static_cast<_Float16*>(packed), static_cast<int>(hidden),
+                       static_cast<int>(inter), pieces);
+  else
+    hipLaunchKernelGGL(k_moe_gu_pack<__bf16>, grid, dim3(256), 0, st, static_cast<const __bf16*>(w), w_expert_stride,
+                       w_row_stride, static_cast<__bf16*>(packed), static_cast<int>(hidden), static_cast<int>(inter),
+                       pieces);
+  return launch_status();
+}
+
+int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
+                                  int dtype, int64_t num_experts, int64_t hidden, int64_t inter,
+                                  const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
+                                  int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
+                                  int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  MoeGuArgs a{};
+  const int rc = moe_setup(a, x, x_row_stride, num_tokens, packed_w, 0, 0, true, dtype, num_experts, hidden, inter,
+                           sorted_ids, block_expert, num_blocks, num_valid, top_k, num_splits, workspace,
+                           workspace_bytes, out, out_row_stride);
+  if (rc != EMBER_OK) return rc;
+  const dim3 grid = moe_grid(num_blocks, inter, num_splits);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16) {
+    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES>), grid, dim3(kGuWaves * kWave), 0,
+                       st, a);
+  } else {
+    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES>), grid, dim3(kGuWaves * kWave), 0,
+                       st, a);
   }
   return launch_status();
 }

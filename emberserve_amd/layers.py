@@ -45,17 +45,37 @@ class SwiGLUMLP(nn.Module):
     [2I, H] with gate rows first, `down_proj` [H, I], no biases), so checkpoints load
     unchanged; the forward runs gate_up_silu (the fused kernel at decode batches, the
     unfused pair otherwise). The tensor-parallel all-reduce after down_proj stays the
-    caller's, as in the reference's `tpdist.all_reduce(...)`."""
+    caller's, as in the reference's `tpdist.all_reduce(...)`.
+
+    `pack_weights()`, called once after the weights are loaded, adds a packed copy of
+    gate_up_proj's weight (the same number of bytes again, outside the state dict) that the
+    decode kernel streams faster; the copy is dropped when the weight tensor is replaced or
+    modified in place, and the forward then reads the weight itself."""
 
     def __init__(self, hidden_size: int, intermediate_size: int) -> None:
         super().__init__()
         self.intermediate_size = intermediate_size
         self.gate_up_proj = nn.Linear(hidden_size, 2 * intermediate_size, bias=False)
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+        self._packed = None
+        self._packed_of = None  # (data_ptr, version) of the weight the copy was made from
+
+    def _weight_key(self):
+        w = self.gate_up_proj.weight
+        return (w.data_ptr(), w._version)
+
+    @torch.no_grad()
+    def pack_weights(self, num_workgroups: int | None = None) -> None:
+        from .gate_up_silu import pack_gate_up_weight
+        self._packed = pack_gate_up_weight(self.gate_up_proj.weight.detach(), num_workgroups)
+        self._packed_of = self._weight_key()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         from .gate_up_silu import gate_up_silu
-        return self.down_proj(gate_up_silu(x, self.gate_up_proj.weight))
+        packed = self._packed
+        if packed is not None and self._packed_of != self._weight_key():
+            self._packed = self._packed_of = packed = None
+        return self.down_proj(gate_up_silu(x, self.gate_up_proj.weight, packed=packed))
 
 
 def qwen3_pre_attention_rope(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,

@@ -78,17 +78,25 @@ def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tup
     return sorted_ids, block_expert, num_valid
 
 
-def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, device: torch.device) -> int:
-    """k splits from shapes only: 2 while the workgroups of the blocks that can hold
-    assignments (at most min(num_valid, num_experts) experts are used) over the 64-column
-    slabs number under 1.5x the CUs, else 1 (>= 2 k steps per split). Measured at
-    Moonlight's geometry (µs, 1 / 2 / 4 splits): one token 17.5 / 15.9 / 16.8, two 31.5 /
-    25.5 / 30.0, three 40.1 / 44.4 / 46.6, four 48.7 / 54.3 / 55.0."""
+def _busy(num_valid: int, num_experts: int, inter: int) -> int:
+    """Workgroups over the blocks that can hold assignments (at most min(num_valid,
+    num_experts) experts are used) and the 64-column slabs, for one k split."""
+    return min(num_valid, num_experts) * max(1, inter // 64)
+
+
+def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, device: torch.device,
+                   packed: bool = False) -> int:
+    """k splits from shapes only (>= 2 k steps per split). Row kernel: 1 while the busy
+    workgroups number under the CUs, else 2. Packed kernel: 1. Measured at Moonlight's
+    geometry with the weights rotated past the Infinity Cache (µs at 1 / 2 / 4 splits;
+    row | packed): 1 token 18.0 / 20.0 / 19.9 | 15.4 / 20.3 / 19.0;  2 tokens 37.3 / 32.5 /
+    31.8 | 32.3 / 31.0 / 30.3;  3 tokens 43.0 / 41.1 / 41.4 | 34.7 / 35.6 / 37.9;  4 tokens
+    52.2 / 48.0 / 52.3 | 40.1 / 44.6 / 47.5;  8 tokens 86.2 / 70.9 / 75.0 | 57.7 / 65.1 /
+    68.3;  64 tokens 147.0 / 137.2 / 155.5 | 112.6 / 137.9 / 154.9."""
     steps = hidden // 64
-    busy = min(num_valid, num_experts) * max(1, inter // 64)
-    if steps % 2 == 0 and steps // 2 >= 2 and busy < 1.5 * num_sms(device):
-        return 2
-    return 1
+    if packed or steps % 2 or steps // 2 < 2:
+        return 1
+    return 1 if _busy(num_valid, num_experts, inter) < num_sms(device) else 2
 
 
 def _workspace_bytes(splits: int, num_valid: int, inter: int, num_blocks: int) -> int:
@@ -118,10 +126,48 @@ def moe_gate_up_silu_torch(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, blo
     return act
 
 
+class PackedExperts:
+    """The routed experts' gate_up weights [E, 2I, H] rearranged for
+    `ember_moe_gate_up_silu_packed`: per expert, 16 KiB units of MFMA operand fragments in
+    k-major order, so the workgroups of one expert read adjacent units. Made once per weight
+    by `pack_moe_gate_up_weight`; the same bytes as the weight."""
+
+    def __init__(self, packed: Tensor, num_experts: int, hidden: int, inter: int) -> None:
+        self.packed, self.num_experts, self.hidden, self.inter = packed, num_experts, hidden, inter
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.packed.dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.packed.device
+
+
+def pack_moe_gate_up_weight(w_gate_up: Tensor) -> PackedExperts:
+    """The packed copy of w_gate_up [E, 2I, H] (fp16/bf16 on the GPU, H and I multiples of 64)."""
+    if w_gate_up.dim() != 3 or w_gate_up.shape[1] % 2 or w_gate_up.dtype not in SUPPORTED_DTYPES:
+        raise ValueError(f"pack_moe_gate_up_weight: an [E, 2I, H] fp16/bf16 weight expected, got "
+                         f"{tuple(w_gate_up.shape)} {w_gate_up.dtype}")
+    _require_device("pack_moe_gate_up_weight", w_gate_up)
+    E, two_i, H = w_gate_up.shape
+    if (H % 64 or (two_i // 2) % 64 or w_gate_up.stride(2) != 1 or w_gate_up.stride(1) % 8
+            or w_gate_up.stride(0) % 8 or w_gate_up.data_ptr() % 16):
+        raise ValueError("pack_moe_gate_up_weight: H and I must be multiples of 64, rows unit-stride and 16-byte "
+                         "aligned")
+    packed = torch.empty(E * two_i * H, dtype=w_gate_up.dtype, device=w_gate_up.device)
+    _launch("ember_moe_gate_up_silu_pack_weight", _lib.load().ember_moe_gate_up_silu_pack_weight, w_gate_up.device,
+            w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1), _lib.dtype_tag(w_gate_up.dtype), E, H,
+            two_i // 2, packed.data_ptr())
+    return PackedExperts(packed, E, H, two_i // 2)
+
+
 def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
-                     top_k: int, *, num_splits: int | None = None) -> Tensor:
+                     top_k: int, *, num_splits: int | None = None, packed: PackedExperts | None = None) -> Tensor:
     """act [num_valid, I]: act[id] = silu_and_mul(x[id // top_k] @ w_gate_up[e].T) for every
-    assignment id in a block of expert e (moe_triton.py:339-340, fused)."""
+    assignment id in a block of expert e (moe_triton.py:339-340, fused). With `packed`
+    (`pack_moe_gate_up_weight(w_gate_up)`), the kernel reads the packed copy instead (the same
+    bits)."""
     assert x.dim() == 2 and w_gate_up.dim() == 3 and w_gate_up.shape[2] == x.shape[1], (x.shape, w_gate_up.shape)
     assert w_gate_up.shape[1] % 2 == 0
     assert sorted_ids.dtype == torch.int32 and block_expert.dtype == torch.int32
@@ -141,8 +187,11 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
             and sorted_ids.is_contiguous() and block_expert.is_contiguous())
     if not fits:
         return moe_gate_up_silu_torch(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+    if packed is not None and (packed.num_experts, packed.hidden, packed.inter, packed.dtype,
+                               packed.device) != (E, H, inter, x.dtype, x.device):
+        raise ValueError("moe_gate_up_silu: the packed weight does not match x and w_gate_up")
     if num_splits is None:
-        num_splits = moe_num_splits(num_valid, E, H, inter, x.device)
+        num_splits = moe_num_splits(num_valid, E, H, inter, x.device, packed=packed is not None)
     num_splits = int(num_splits)
     if num_splits not in (1, 2, 4) or (H // 64) % num_splits or H // 64 // num_splits < 2:
         raise ValueError(f"moe_gate_up_silu: num_splits {num_splits} must be 1, 2 or 4 and divide hidden / 64 "
@@ -152,11 +201,17 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
     if num_splits > 1:
         ws = _SCRATCH.get((num_splits, num_valid, inter, nb), lambda: _workspace_bytes(num_splits, num_valid, inter, nb),
                           x.device)
-    _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
-            x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
-            _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
-            block_expert.numel(), num_valid, top_k, num_splits, ws.data_ptr() if ws is not None else None,
-            ws.numel() * 4 if ws is not None else 0, out.data_ptr(), out.stride(0))
+    ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel() * 4) if ws is not None else (None, 0)
+    if packed is not None:
+        _launch("ember_moe_gate_up_silu_packed", _lib.load().ember_moe_gate_up_silu_packed, x.device,
+                x.data_ptr(), x.stride(0), x.shape[0], packed.packed.data_ptr(), _lib.dtype_tag(x.dtype), E, H, inter,
+                sorted_ids.data_ptr(), block_expert.data_ptr(), block_expert.numel(), num_valid, top_k, num_splits,
+                ws_ptr, ws_bytes, out.data_ptr(), out.stride(0))
+    else:
+        _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
+                x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
+                _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
+                block_expert.numel(), num_valid, top_k, num_splits, ws_ptr, ws_bytes, out.data_ptr(), out.stride(0))
     if _check_indices():
         if ws is not None:
             need, cnt = _workspace_bytes(num_splits, num_valid, inter, nb), nb * (inter // 64)
@@ -166,9 +221,10 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
     return out
 
 
-def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None) -> Tensor:
+def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None,
+                      packed: PackedExperts | None = None) -> Tensor:
     """moe_align + moe_gate_up_silu: the routed experts' activations [N * k, I] in
     assignment order (the `act` of moe_triton.py:341)."""
     sorted_ids, block_expert, num_valid = moe_align(topk_ids, w_gate_up.shape[0])
     return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1],
-                            num_splits=num_splits)
+                            num_splits=num_splits, packed=packed)

@@ -390,12 +390,36 @@ int ember_gate_up_silu(const void* x, int64_t x_row_stride, const void* w, int64
  * multiples of 64. A row id / top_k >= num_tokens reads row 0 and sets
  * EMBER_ERR_ROW_INDEX. num_splits (1..4, dividing hidden / 64 with >= 2 steps per split)
  * splits k across workgroups for small batches; with more than one it needs a zero-filled
- * workspace of ember_moe_gate_up_silu_workspace_bytes, whose counters it leaves at zero. */
+ * workspace of ember_moe_gate_up_silu_workspace_bytes, whose counters it leaves at zero.
+ * num_blocks <= 65535 (EMBER_EINVAL beyond). */
 int ember_moe_gate_up_silu(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
                            int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
                            int64_t hidden, int64_t inter, const int32_t* sorted_ids, const int32_t* block_expert,
                            int64_t num_blocks, int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
                            int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+
+/* Rearranges the routed experts' gate_up weights W [E, 2I, H] (element strides
+ * w_expert_stride, w_row_stride; fp16 or bf16, 16-byte aligned; H and I multiples of 64)
+ * into the layout ember_moe_gate_up_silu_packed reads: E * 2 I H elements, expert e at
+ * e * 2 I H, and in it unit (j, slab) (j < H / 64, slab < I / 64) at (j * I / 64 + slab) *
+ * 8192, holding
+ *   unit[h][wave][part][lane][8] = W[e][part I + 64 slab + 16 wave + lane % 16]
+ *                                   [64 j + 32 h + 8 (lane / 16) + 0..7]
+ * (h < 2, wave < 4, part 0 gate / 1 up, lane < 64). A pure permutation, done once per
+ * weight (at load time). No counterpart in the reference: the layout is this library's. */
+int ember_moe_gate_up_silu_pack_weight(const void* w, int64_t w_expert_stride, int64_t w_row_stride, int dtype,
+                                       int64_t num_experts, int64_t hidden, int64_t inter, void* packed,
+                                       void* stream);
+
+/* ember_moe_gate_up_silu over weights packed by ember_moe_gate_up_silu_pack_weight: the same
+ * arguments less the weight strides, the same workspace, limits and errors, and the same
+ * results bit for bit (the same products in the same order); replaces the same reference
+ * calls (moe_triton.py:332-345). */
+int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
+                                  int dtype, int64_t num_experts, int64_t hidden, int64_t inter,
+                                  const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
+                                  int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
+                                  int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
 
 /* Rearranges a gate_up weight W [2I, H] (row stride w_row_stride elements, fp16 or bf16,
  * 16-byte aligned) into the layout ember_gate_up_silu_packed reads with num_workgroups

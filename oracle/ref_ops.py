@@ -44,6 +44,7 @@ How each function is pinned (tests/test_oracle.py), beyond this restatement:
                                that expert's weight, row by row; rows follow the assignment
                                order t * k + c; experts are picked by index, not position.
   pack_gate_up_weight          an element-by-element index definition on a small weight.
+  pack_moe_gate_up_weight      the same, per expert.
   moe_align                    the reference's own layout case (tests/test_moe_triton.py:
                                34-48) written out slot by slot; every assignment exactly once;
                                runs ascending and block-aligned; sizes; all-one-expert and
@@ -125,6 +126,17 @@ def pack_gate_up_weight(weight: torch.Tensor, num_workgroups: int) -> torch.Tens
     runs = [list(range(b * total // g, (b + 1) * total // g)) for b in range(g)]
     order = [run[t] for t in range(max(len(r) for r in runs)) for run in runs if t < len(run)]
     return units[torch.tensor(order)].reshape(-1)
+
+
+def pack_moe_gate_up_weight(w_gate_up: torch.Tensor) -> torch.Tensor:
+    """The packed routed-expert gate_up layout of this library (no counterpart in the
+    reference; a permutation of W [E, 2I, H]): per expert, units (j, slab) in j-major order,
+    each unit[h][wave][part][lane][8] = W[e][part I + 64 slab + 16 wave + lane % 16]
+    [64 j + 32 h + 8 (lane // 16) + e8]."""
+    ne, two_i, h = w_gate_up.shape
+    i = two_i // 2
+    v = w_gate_up.reshape(ne, 2, i // 64, 4, 16, h // 64, 2, 4, 8)  # E, part, slab, wave, n, j, h, g, e8
+    return v.permute(0, 5, 2, 6, 3, 1, 7, 4, 8).reshape(-1)        # E, j, slab, h, wave, part, g, n, e8
 
 
 def moe_gate_up_silu(x: torch.Tensor, topk_ids: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:

@@ -212,3 +212,21 @@ def test_packed_weight_rejects_another_grid():
     packed = pack_gate_up_weight(w, 3)
     with pytest.raises(ValueError, match="packed for 3"):
         gate_up_silu(x, w, num_workgroups=4, fused=True, packed=packed)
+
+
+def test_swiglu_mlp_packed_weights():
+    """SwiGLUMLP.pack_weights: the packed path gives the unpacked module's output bit for bit,
+    and an in-place change of the weight drops the stale copy."""
+    from emberserve_amd import layers
+    torch.manual_seed(1)
+    mlp = layers.SwiGLUMLP(1024, 512).to(DEV, torch.bfloat16)
+    x = torch.randn(4, 1024, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        want = mlp(x)
+        mlp.pack_weights()
+        assert mlp._packed is not None
+        assert torch.equal(mlp(x), want)
+        mlp.gate_up_proj.weight.mul_(2)
+        changed = mlp(x)
+        assert mlp._packed is None
+        assert torch.equal(changed, mlp.down_proj(gate_up_silu(x, mlp.gate_up_proj.weight)))

@@ -416,10 +416,14 @@ def test_moe_split_rule_and_workspace(monkeypatch):
     from emberserve_amd import moe
     monkeypatch.setattr(moe, "num_sms", lambda device: 256)
     dev = torch.device("cpu")
-    assert moe.moe_num_splits(6, 64, 2048, 1408, dev) == 2     # one token: 6 x 22 slabs = 132
-    assert moe.moe_num_splits(12, 64, 2048, 1408, dev) == 2    # two tokens: 264 < 384
-    assert moe.moe_num_splits(18, 64, 2048, 1408, dev) == 1    # three tokens: 396
-    assert moe.moe_num_splits(48, 64, 2048, 1408, dev) == 1    # eight tokens
+    # row kernel: one split under the CUs, else two
+    assert moe.moe_num_splits(6, 64, 2048, 1408, dev) == 1     # one token: 6 x 22 slabs = 132
+    assert moe.moe_num_splits(12, 64, 2048, 1408, dev) == 2    # two tokens: 264
+    assert moe.moe_num_splits(384, 64, 2048, 1408, dev) == 2   # 64 tokens: 1408
+    # packed kernel: one split
+    assert moe.moe_num_splits(6, 64, 2048, 1408, dev, packed=True) == 1
+    assert moe.moe_num_splits(12, 64, 2048, 1408, dev, packed=True) == 1
+    assert moe.moe_num_splits(12, 64, 64 * 3, 1408, dev) == 1  # three k steps: no even split
     lib = _lib.load()
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 1) == 0
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 4) == (4 * 6 * 2816 * 4 + 255) // 256 * 256 + (61 * 22 * 4 + 255) // 256 * 256

@@ -16,7 +16,7 @@ if not torch.cuda.is_available():
     pytest.skip("needs a GPU", allow_module_level=True)
 
 from emberserve_amd import _lib  # noqa: E402
-from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu  # noqa: E402
+from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu, pack_moe_gate_up_weight  # noqa: E402
 from oracle import ref_ops as ref  # noqa: E402
 from tests.helpers import check_gate_up  # noqa: E402
 
@@ -101,5 +101,41 @@ def test_moe_gate_up_bad_assignment_sets_error_bit():
     x, w, ids = _inputs(4, torch.bfloat16, seed=2)
     sorted_ids, block_expert, nv = moe_align(ids.to(DEV), E)
     moe_gate_up_silu(x[:2].to(DEV), w.to(DEV), sorted_ids, block_expert, nv, K)  # rows 2, 3 missing
+    torch.cuda.synchronize()
+    assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX
+
+
+# ---- the packed expert layout (ember_moe_gate_up_silu_pack_weight / _packed) ----
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_moe_pack_weight_matches_the_oracle_permutation(dtype):
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(5, 2 * 192, 256, generator=g).to(dtype)
+    got = pack_moe_gate_up_weight(w.to(DEV)).packed.cpu()
+    assert torch.equal(got.view(torch.int16), ref.pack_moe_gate_up_weight(w).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 2, 8, 37])
+def test_moe_packed_equals_the_row_kernel(dtype, n):
+    """Same grid, products and order: bit-identical to ember_moe_gate_up_silu at every split
+    count, and within the oracle's tolerance."""
+    print(f"moe packed n={n} {dtype}", flush=True)
+    x, w, ids = _inputs(n, dtype, seed=100 + n)
+    dx, dids, dw = x.to(DEV), ids.to(DEV), w.to(DEV)
+    packed = pack_moe_gate_up_weight(dw)
+    sorted_ids, block_expert, nv = moe_align(dids, E)
+    for splits in (1, 2, 4):
+        a = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=splits)
+        b = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=splits, packed=packed)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"n={n} splits={splits}"
+    if n <= 8:
+        _check(fused_moe_gate_up(dx, dids, dw, packed=packed), x, w, ids, f"packed n={n}")
+
+
+def test_moe_packed_bad_assignment_sets_error_bit():
+    x, w, ids = _inputs(4, torch.bfloat16, seed=2)
+    dw = w.to(DEV)
+    sorted_ids, block_expert, nv = moe_align(ids.to(DEV), E)
+    moe_gate_up_silu(x[:2].to(DEV), dw, sorted_ids, block_expert, nv, K, packed=pack_moe_gate_up_weight(dw))
     torch.cuda.synchronize()
     assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX

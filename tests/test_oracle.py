@@ -678,3 +678,23 @@ def test_pack_gate_up_weight_index_definition(groups):
                 col = 64 * j + 32 * hh + 8 * (lane // 16) + e
                 assert float(p[base + idx]) == float(w[row, col]), (groups, slab, j, idx)
     assert sorted(p.tolist()) == list(range(w.numel()))  # a permutation
+
+
+def test_pack_moe_gate_up_weight_index_definition():
+    """Element by element: expert e at e * 2 I H, unit (j, slab) at (j * I / 64 + slab) * 8192,
+    holding W[e][part I + 64 slab + 16 wave + lane % 16][64 j + 32 h + 8 (lane // 16) + e8] at
+    ((h * 4 + wave) * 2 + part) * 64 + lane."""
+    ne, i, h = 3, 128, 192
+    w = torch.arange(ne * 2 * i * h, dtype=torch.float64).view(ne, 2 * i, h)
+    p = ref.pack_moe_gate_up_weight(w)
+    slabs = i // 64
+    for e in range(ne):
+        for j in range(h // 64):
+            for slab in range(slabs):
+                base = e * 2 * i * h + (j * slabs + slab) * 8192
+                for idx in range(0, 8192, 31):
+                    e8, lane, part, wave, hh = idx % 8, idx // 8 % 64, idx // 512 % 2, idx // 1024 % 4, idx // 4096
+                    row = part * i + 64 * slab + 16 * wave + lane % 16
+                    col = 64 * j + 32 * hh + 8 * (lane // 16) + e8
+                    assert float(p[base + idx]) == float(w[e, row, col]), (e, j, slab, idx)
+    assert sorted(p.tolist()) == list(range(w.numel()))
