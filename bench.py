@@ -145,14 +145,19 @@ def _ops(torch, ops, tables):
     dev = torch.device("cuda")
     bf, f16 = torch.bfloat16, torch.float16
     g = torch.Generator(device=dev)
+    gi = torch.Generator()  # integer draws (ids, positions, slots) on the host, then copied
+
+    def seed(s):
+        g.manual_seed(s)
+        gi.manual_seed(s)
 
     def randn(shape, dtype, seed, mean=0.0, std=1.0):
         g.manual_seed(seed)
         return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
 
     def randint(n, high, seed):
-        g.manual_seed(seed)
-        return torch.randint(0, high, (n,), generator=g, device=dev)
+        gi.manual_seed(seed)
+        return torch.randint(0, high, (n,), generator=gi).to(dev)
 
     out = []
 
@@ -229,8 +234,8 @@ def _ops(torch, ops, tables):
 
         def make(i):
             qkv = randn((t, 6144), bf, 50 + i)
-            g.manual_seed(60 + i)
-            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            seed(60 + i)
+            slots = torch.randperm(blocks * bs, generator=gi).to(dev)[:t]
             kc = torch.zeros((blocks, bs, 8, 128), dtype=bf, device=dev)
             return (qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128), slots, kc, torch.zeros_like(kc))
         nbytes = 4 * t * 8 * 128 * 2 + 8 * t
@@ -244,8 +249,8 @@ def _ops(torch, ops, tables):
 
         def make(i):
             qkv = randn((t, 6144), bf, 70 + i)
-            g.manual_seed(80 + i)
-            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            seed(80 + i)
+            slots = torch.randperm(blocks * bs, generator=gi).to(dev)[:t]
             kc = torch.zeros((blocks, bs, 8, 128), dtype=bf, device=dev)
             return (qkv[:, :4096].view(t, 32, 128), qkv[:, 4096:5120].view(t, 8, 128), qkv[:, 5120:].view(t, 8, 128),
                     randint(t, 40960, 90 + i), slots, kc, torch.zeros_like(kc),
@@ -260,8 +265,8 @@ def _ops(torch, ops, tables):
         blocks, bs = 2 * t // 16, 16
 
         def make(i):
-            g.manual_seed(95 + i)
-            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            seed(95 + i)
+            slots = torch.randperm(blocks * bs, generator=gi).to(dev)[:t]
             return (randn((t, 576), bf, 96 + i), slots, torch.zeros((blocks, bs, 576), dtype=bf, device=dev))
         nbytes = 2 * t * 576 * 2 + 8 * t
         out.append(Op("latent_cache_write", cfg, f"latent[{t},576] bf16 -> paged cache", nbytes, make,
@@ -312,8 +317,8 @@ def _ops(torch, ops, tables):
         def make(i):
             kv_a = randn((t, 576), bf, 120 + i)
             q = randn((t, 16, 192), bf, 130 + i)
-            g.manual_seed(140 + i)
-            slots = torch.randperm(blocks * bs, generator=g, device=dev)[:t]
+            seed(140 + i)
+            slots = torch.randperm(blocks * bs, generator=gi).to(dev)[:t]
             return (kv_a[:, :512], kv_a[:, 512:], q[..., 128:], randn((512,), bf, 150, 1.0, 0.1),
                     randint(t, 8192, 160 + i), slots, torch.zeros((blocks, bs, 576), dtype=bf, device=dev))
         nbytes = t * 6408 + 1024 + t * (576 * 2 + 8)  # the MLA bytes + the cache rows and slots
@@ -332,8 +337,8 @@ def _ops(torch, ops, tables):
         def make(i):
             kc = randn((nblk, bs, hkv, d), dtype, 210 + i)
             vc = randn((nblk, bs, hkv, d), dtype, 220 + i)
-            g.manual_seed(200 + i)  # scrambled block tables (bench_kernels.py:55-80)
-            bt = torch.randperm(nblk, generator=g, device=dev)[: b * per].to(torch.int32).view(b, per)
+            seed(200 + i)  # scrambled block tables (bench_kernels.py:55-80)
+            bt = torch.randperm(nblk, generator=gi).to(dev)[: b * per].to(torch.int32).view(b, per)
             return (randn((b, hq, d), dtype, 230 + i), kc, vc, bt,
                     torch.full((b,), ctx, dtype=torch.int32, device=dev))
         kv_bytes = b * ctx * hkv * d * 2 * e
@@ -350,8 +355,8 @@ def _ops(torch, ops, tables):
 
         def make(i):
             lat = randn((nblk, bs, dl + dr), bf, 240 + i, std=0.5)
-            g.manual_seed(250 + i)  # scrambled block tables
-            bt = torch.randperm(nblk, generator=g, device=dev)[: b * per].to(torch.int32).view(b, per)
+            seed(250 + i)  # scrambled block tables
+            bt = torch.randperm(nblk, generator=gi).to(dev)[: b * per].to(torch.int32).view(b, per)
             return (randn((b, h, dl + dr), bf, 260 + i, std=0.5), lat, bt,
                     torch.full((b,), ctx, dtype=torch.int32, device=dev))
         lat_bytes = b * ctx * (dl + dr) * 2
@@ -388,8 +393,8 @@ def _ops(torch, ops, tables):
         experts' weights (each read once) plus x and the activations."""
         from emberserve_amd.moe import moe_align, moe_gate_up_silu, pack_moe_gate_up_weight
         h, inter, ne, k = 2048, 1408, 64, 6
-        g.manual_seed(290 + n)
-        ids = torch.stack([torch.randperm(ne, generator=g, device=dev)[:k] for _ in range(n)])
+        seed(290 + n)
+        ids = torch.stack([torch.randperm(ne, generator=gi).to(dev)[:k] for _ in range(n)])
         used_ids = torch.unique(ids)
         used = int(used_ids.numel())
         sorted_ids, block_expert, nv = moe_align(ids, ne)
@@ -419,8 +424,8 @@ def _ops(torch, ops, tables):
         """ember_moe_align alone (moe_triton.py:215-254's layout in one launch): bytes are the
         ids read plus the layout written."""
         from emberserve_amd.moe import moe_align
-        g.manual_seed(330 + n)
-        ids = torch.stack([torch.randperm(ne, generator=g, device=dev)[:k] for _ in range(n)])
+        seed(330 + n)
+        ids = torch.stack([torch.randperm(ne, generator=gi).to(dev)[:k] for _ in range(n)])
         nv = n * k
         padded = -(-(nv + ne * 15) // 16) * 16
         nbytes = nv * 8 + padded * 4 + padded // 16 * 4
@@ -553,17 +558,19 @@ def _chain_sets(torch, t, nsets):
     dev = torch.device("cuda")
     bf = torch.bfloat16
     g = torch.Generator(device=dev)
+    gi = torch.Generator()  # integer draws on the host, then copied
     g.manual_seed(12345)
     table = (torch.randn((151936, 4096), generator=g, device=dev) * 0.02).to(bf)
     sets = []
     for i in range(nsets):
         g.manual_seed(100 + i)
+        gi.manual_seed(100 + i)
         sets.append(dict(
-            ids=torch.randint(0, 151936, (t,), generator=g, device=dev),
+            ids=torch.randint(0, 151936, (t,), generator=gi).to(dev),
             qkv=torch.randn((t, 6144), generator=g, device=dev).to(bf),
             qw=(torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf),
             kw=(torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf),
-            pos=torch.randint(0, 40960, (t,), generator=g, device=dev),
+            pos=torch.randint(0, 40960, (t,), generator=gi).to(dev),
             x=torch.randn((t, 4096), generator=g, device=dev).to(bf),
             r=torch.randn((t, 4096), generator=g, device=dev).to(bf),
             w=(torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)))
@@ -596,18 +603,20 @@ def _graph_replay(torch, ops, tables, layers=36, reps=20):
     out = {}
     for t in (1, 256):
         g = torch.Generator(device=dev)
+        gi = torch.Generator()  # integer draws on the host, then copied
         g.manual_seed(7 + t)
+        gi.manual_seed(7 + t)
         x = torch.randn((t, 4096), generator=g, device=dev).to(bf)
         r = torch.randn((t, 4096), generator=g, device=dev).to(bf)
         w = (torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)
         qkv = torch.randn((t, 6144), generator=g, device=dev).to(bf)
         qw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
         kw = (torch.randn(128, generator=g, device=dev) * 0.1 + 1).to(bf)
-        pos = torch.randint(0, 40960, (t,), generator=g, device=dev)
+        pos = torch.randint(0, 40960, (t,), generator=gi).to(dev)
         gu = torch.randn((t, 2 * 12288), generator=g, device=dev).to(bf)
         kc = torch.zeros((1024, 16, 8, 128), device=dev, dtype=bf)
         vc = torch.zeros_like(kc)
-        slots = torch.randperm(1024 * 16, generator=g, device=dev)[:t]
+        slots = torch.randperm(1024 * 16, generator=gi).to(dev)[:t]
 
         def step():
             for _ in range(layers):
@@ -673,7 +682,9 @@ def _graph_decode_step(torch, ops, tables, layers=36, reps=10, batch=64, ctx=204
     for _ in range(layers):
         kc = torch.randn((nblk, 16, 8, 128), generator=g, device=dev).to(bf)
         caches.append((kc, torch.randn_like(kc)))
-    bt = torch.randperm(nblk, generator=g, device=dev)[:t * per].to(torch.int32).view(t, per)
+    gi = torch.Generator()  # integer draws on the host, then copied
+    gi.manual_seed(91)
+    bt = torch.randperm(nblk, generator=gi).to(dev)[:t * per].to(torch.int32).view(t, per)
     cl = torch.full((t,), ctx, dtype=torch.int32, device=dev)
     pos = torch.full((t,), ctx - 1, dtype=torch.int64, device=dev)
     slots = (bt[:, (ctx - 1) // 16].to(torch.int64) * 16 + (ctx - 1) % 16).contiguous()
