@@ -44,6 +44,10 @@
 #ifndef EMBER_GU_PACKED_STAGES
 #define EMBER_GU_PACKED_STAGES 3
 #endif
+// Token tiles up to which the packed kernel loads x per wave from L2 (above: shared in LDS).
+#ifndef EMBER_GU_PACKED_PRIVX_MT
+#define EMBER_GU_PACKED_PRIVX_MT 1
+#endif
 // Ring stages of the routed-expert kernel (one workgroup per block and slab, not persistent).
 // Measured at Moonlight's geometry: 2 stages (48 KB of LDS, three workgroups per CU) are
 // 5-10% slower than 3 at 1-64 tokens (8 tokens: 98.8 vs 89.6 us).
@@ -267,7 +271,7 @@ struct GuRun {
       f32x4 sum[MT][2];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) sum[mt][0] = sum[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      constexpr int SB = 4;  // partials per batch of loads
+      constexpr int SB = MT <= 4 ? 4 : (MT <= 8 ? 2 : 1);  // partials per batch of loads (registers)
       for (int64_t p0 = 0; p0 < parts; p0 += SB) {
         f32x4 v[SB][MT][2];
 #pragma unroll
@@ -501,6 +505,109 @@ k_gate_up_silu_packed(GuArgs a) {
   run.merge(last_flags);
 }
 
+// The packed kernel for 17-64 tokens. Per unit, every wave needs the x slice of all tokens
+// (MT token tiles, 2 KiB each per 64-k step); loading it per lane from L2, as
+// k_gate_up_silu_packed does, reads 4 copies per unit and stops scaling past 16 tokens
+// (Qwen3-8B: 42 us at 32 tokens, 66 at 64). Here the four waves share one copy in an LDS
+// ring, in the B-operand fragment order (fragment f = 2 mt + h of a unit at f KiB, lane
+// (n, g) at 16 lane: token 16 mt + n, k 32 h + 8 g + [0, 8)), each wave direct-loading a
+// quarter of the fragments. Per unit: wait for this wave's loads of it (a counted vmcnt:
+// NS - 2 later stages stay in flight), a barrier (every wave's x of it has landed, and every
+// wave is done with the stage the next issue overwrites), the next issue, the MFMAs. The
+// weights stream through the register ring of k_gate_up_silu_packed, with the same units,
+// runs, epilogue and merge, so each token's result is bit-identical to the other kernels'.
+// Measured on MI355X (Qwen3-8B / Qwen2.5-7B): 37.1 / 52.0 us at 32 tokens, 44.5 / 65.0 at 64.
+// 8 and 16 token tiles (up to 256 tokens) were built and measured slower than hipBLASLt +
+// silu_and_mul (Qwen3-8B at 128 tokens 64.1 vs 54.7 us, at 256 tokens 128.1 vs 74.7): every
+// wave reads every token's x from LDS and runs MFMAs for all of them, which grows with T
+// past the weight stream.
+template <typename T, int MT, int NS>
+__global__ void __launch_bounds__(kGuWaves * kWave, 1)
+k_gate_up_silu_packed_x(GuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  static_assert(MT % 2 == 0 && MT <= 4, "token tiles");
+  static_assert(NS >= 2 && NS <= 4, "stages");
+  constexpr int XF = MT / 2;          // x fragments each wave loads per unit
+  constexpr int LPS = 4 + XF;         // loads per wave per unit
+  static_assert(LPS * (NS - 1) < 64, "vmcnt");
+  constexpr int XSTAGE = MT * 2 * 1024;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[NS * XSTAGE];
+  __shared__ int last_flags[kGuMaxFlush];
+  const int64_t nk = a.H / kGuBK;
+  const int64_t total = static_cast<int64_t>(a.I / kGuSlab) * nk;
+  const int64_t u0 = gu_start(blockIdx.x, total, gridDim.x);
+  const int nu = static_cast<int>(gu_start(blockIdx.x + 1, total, gridDim.x) - u0);  // >= 1
+  GuRun<T, MT> run(a, u0);
+  const int lane = run.lane, w = run.w, n = run.n, g = run.g;
+
+  const T* wp = static_cast<const T*>(a.w) + (w * 2 * kWave + lane) * 8;
+  const T* xsrc[XF];
+  int xdst[XF];
+#pragma unroll
+  for (int i = 0; i < XF; ++i) {
+    const int f = w + kGuWaves * i;  // fragment 2 mt + h
+    const int mt = f >> 1, h = f & 1;
+    xsrc[i] = static_cast<const T*>(a.x) + static_cast<int64_t>(min(16 * mt + n, a.T - 1)) * a.xs + 32 * h + 8 * g;
+    xdst[i] = f * 1024;
+  }
+
+  struct Stage {
+    V8 wgt[2], wup[2];
+  };
+  Stage ring[NS];
+  auto issue = [&](Stage& st, int d, int j) {
+    const int t = min(j, nu - 1);  // past the run: repeat its last unit
+    const int64_t kk = ((u0 + t) % nk) * kGuBK;
+    const T* up = wp + gu_packed_pos(blockIdx.x, t, total, gridDim.x) * (2 * kGuWaves * 2 * kWave * 8);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const T* f = up + h * (kGuWaves * 2 * kWave * 8);
+      st.wgt[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f));
+      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(f + kWave * 8));
+    }
+    unsigned char* xs = lds + d * XSTAGE;
+#pragma unroll
+    for (int i = 0; i < XF; ++i) gu_load_lds16(xsrc[i] + kk, xs + xdst[i]);
+  };
+  f32x4 acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int d = 0; d < NS - 1; ++d) {
+    issue(ring[d], d, d);
+    __builtin_amdgcn_sched_barrier(0);  // stages issued in ring order, oldest consumed first
+  }
+  for (int j0 = 0; j0 < nu; j0 += NS) {
+#pragma unroll
+    for (int d = 0; d < NS; ++d) {
+      const int j = j0 + d;
+      // this wave's loads of unit j are done (the NS - 2 units issued after it may not be),
+      // then every wave's are, and every wave has read the stage the next issue overwrites
+      wait_vm<(NS - 2) * LPS>();
+      gu_barrier();
+      const int dn = (d + NS - 1) % NS;  // a constant once the loop is unrolled
+      issue(ring[dn], dn, j + NS - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < nu) {  // uniform
+        const unsigned char* xs = lds + d * XSTAGE + lane * 16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const V8 xv = *reinterpret_cast<const V8*>(xs + (2 * mt + h) * 1024);
+            acc[mt][0] = M::run(ring[d].wgt[h], xv, acc[mt][0]);
+            acc[mt][1] = M::run(ring[d].wup[h], xv, acc[mt][1]);
+          }
+        }
+        run.template end_unit<true>(j, nu, acc);
+      }
+    }
+  }
+  run.merge(last_flags);
+}
+
 // Packs W [2I, H] (row stride ws) into the layout of k_gate_up_silu_packed for a grid of G
 // workgroups: thread t of the grid moves the 16-byte piece t of the unit-major order
 // ((((slab * nk32 + step) * 4 + wave) * 2 + part) * 64 + lane) to its unit's packed place.
@@ -542,15 +649,22 @@ int launch_gu_packed(const GuArgs& a, int64_t programs, hipStream_t st) {
   return launch_status();
 }
 
+template <typename T, int MT>
+int launch_gu_packed_x(const GuArgs& a, int64_t programs, hipStream_t st) {
+  hipLaunchKernelGGL((k_gate_up_silu_packed_x<T, MT, EMBER_GU_PACKED_STAGES>), dim3(static_cast<uint32_t>(programs)),
+                     dim3(kGuWaves * kWave), 0, st, a);
+  return launch_status();
+}
+
+// Up to 16 tokens each wave loads its own x (k_gate_up_silu_packed); above, the waves share
+// it through LDS (k_gate_up_silu_packed_x), with the token tiles padded to 2 or 4.
 template <typename T>
 int launch_gu_packed_typed(const GuArgs& a, int64_t programs, hipStream_t st) {
-  switch ((a.T + 15) / 16) {
-    case 1: return launch_gu_packed<T, 1>(a, programs, st);
-    case 2: return launch_gu_packed<T, 2>(a, programs, st);
-    case 3: return launch_gu_packed<T, 3>(a, programs, st);
-    case 4: return launch_gu_packed<T, 4>(a, programs, st);
-    default: return EMBER_EINVAL;
-  }
+  const int tiles = (a.T + 15) / 16;
+  if (tiles <= EMBER_GU_PACKED_PRIVX_MT) return launch_gu_packed<T, 1>(a, programs, st);
+  if (tiles <= 2) return launch_gu_packed_x<T, 2>(a, programs, st);
+  if (tiles <= 4) return launch_gu_packed_x<T, 4>(a, programs, st);
+  return EMBER_EINVAL;
 }
 
 template <typename T>
@@ -564,8 +678,11 @@ int launch_gu_typed(const GuArgs& a, int64_t programs, hipStream_t st) {
   }
 }
 
+// One slab partial: the token tiles rounded up to a power of two, the most any kernel pads
+// them to (the row kernels use the exact count, the LDS-x packed kernel 2, 4, 8 or 16).
 int64_t gu_partial_floats(int64_t tokens) {
-  const int64_t mt = (tokens + 15) / 16;
+  int64_t mt = 1;
+  while (mt < (tokens + 15) / 16) mt *= 2;
   return kGuWaves * mt * 2 * kWave * 4;
 }
 

@@ -15,7 +15,10 @@ faster than the unfused pair (torch's linear, i.e. hipBLASLt, then this library'
 silu_and_mul) on MI355X: Qwen3-8B (H 4096, I 12288) 40 vs 45 us at 1-16 tokens, Qwen2.5-7B
 (H 3584, I 18944) 54.5 vs 54.8 us. From 32 tokens on the library GEMM was as fast or faster,
 so the unfused pair runs there; `fused=True` forces the kernel (up to 64 tokens) and
-`fused=False` the pair. Where the kernel does not apply (more than 64 tokens, fp32, shapes
+`fused=False` the pair. Over a weight packed at load time (`packed=`) the kernel runs by
+default up to PACKED_FUSED_TOKENS: 35.3 vs 46.1 us at 16 tokens and 37.1 vs 45.8 at 32
+(Qwen3-8B), 52.0 vs 56.7 at 32 (Qwen2.5-7B); at 48-64 tokens it is ahead at Qwen3-8B
+(44.5 vs 47.8) and behind at Qwen2.5-7B (65.0 vs 63.0). Where the kernel does not apply (more than 64 tokens, fp32, shapes
 that are not multiples of 64, unaligned operands) the pair runs. CPU tensors, or
 `EMBERSERVE_FUSED_OPS=0`, take the eager forms.
 
@@ -36,8 +39,10 @@ from ._scratch import ScratchCache, round_up
 from .ops import _check_indices, _launch, _require_device, fused_enabled
 from .paged_decode import num_sms
 
-MAX_TOKENS = 64    # the kernel's limit
-FUSED_TOKENS = 16  # default dispatch: the kernel up to here, the unfused pair above
+MAX_TOKENS = 64           # the kernels' limit
+PACKED_MAX_TOKENS = 64
+FUSED_TOKENS = 16         # default dispatch, row kernel: the kernel up to here, the pair above
+PACKED_FUSED_TOKENS = 32  # default dispatch over a packed weight
 SLAB = 64          # output columns per workgroup
 STEP = 64          # k per pipeline stage
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
@@ -64,10 +69,10 @@ def gate_up_silu_torch(x: Tensor, weight: Tensor) -> Tensor:
     return ops.silu_and_mul(F.linear(x, weight))
 
 
-def _fits(x2: Tensor, weight: Tensor, out: Tensor) -> bool:
+def _fits(x2: Tensor, weight: Tensor, out: Tensor, max_tokens: int = MAX_TOKENS) -> bool:
     T, H = x2.shape
     I = weight.shape[0] // 2
-    return (1 <= T <= MAX_TOKENS and x2.dtype == weight.dtype == out.dtype and x2.dtype in SUPPORTED_DTYPES
+    return (1 <= T <= max_tokens and x2.dtype == weight.dtype == out.dtype and x2.dtype in SUPPORTED_DTYPES
             and H % STEP == 0 and I % SLAB == 0 and I >= SLAB
             and x2.stride(1) == 1 and weight.stride(1) == 1 and out.stride(1) == 1
             and x2.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0 and out.stride(0) % 4 == 0
@@ -131,7 +136,8 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     out = torch.empty((T, I), dtype=x.dtype, device=x.device)
     if T == 0:
         return out.view(*x.shape[:-1], I)
-    if fused is False or (fused is None and T > FUSED_TOKENS) or not _fits(x2, weight, out):
+    limit, default = (PACKED_MAX_TOKENS, PACKED_FUSED_TOKENS) if packed is not None else (MAX_TOKENS, FUSED_TOKENS)
+    if fused is False or (fused is None and T > default) or not _fits(x2, weight, out, limit):
         return gate_up_silu_torch(x, weight)
     programs = gate_up_silu_workgroups(x.device) if num_workgroups is None else int(num_workgroups)
     if packed is not None:

@@ -174,7 +174,7 @@ def test_pack_weight_matches_the_oracle_permutation(dtype, programs):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("tokens", [1, 7, 16, 33, 64])
+@pytest.mark.parametrize("tokens", [1, 7, 16, 17, 33, 40, 64])
 @pytest.mark.parametrize("programs", [7, 256, 300])
 def test_packed_kernel_equals_the_row_kernel(dtype, tokens, programs):
     """Same products in the same order: bit-identical to ember_gate_up_silu (Qwen2.5-0.5B

@@ -344,10 +344,13 @@ def test_gate_up_silu_workspace_plan():
         for b in range(G):
             owner += [b] * ((b + 1) * total // G - b * total // G)
         parts = max(len(set(owner[s * nk:(s + 1) * nk])) for s in range(slabs))
-        floats = 4 * -(-tokens // 16) * 2 * 64 * 4
+        tiles = 1
+        while tiles < -(-tokens // 16):  # token tiles rounded up to a power of two
+            tiles *= 2
+        floats = 4 * tiles * 2 * 64 * 4
         return slabs * parts * floats * 4 + (slabs * 4 + 255) // 256 * 256
     for args in [(16, 4096, 12288, 256), (64, 3584, 18944, 256), (1, 896, 4864, 256), (5, 128, 64, 256),
-                 (33, 4096, 12288, 512), (16, 1024, 1024, 7)]:
+                 (33, 4096, 12288, 512), (16, 1024, 1024, 7), (40, 4096, 12288, 256)]:
         assert lib.ember_gate_up_silu_workspace_bytes(*args) == expected(*args), args
     assert lib.ember_gate_up_silu_workspace_bytes(65, 4096, 12288, 256) == -1
     assert lib.ember_gate_up_silu_workspace_bytes(16, 4096, 100, 256) == -1
