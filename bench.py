@@ -489,16 +489,15 @@ def _ops(torch, ops, tables):
     out.append(Op("copy_calibration", "cal", "identity gather [32768,4096] bf16 (256 MiB)", 2 * 2 ** 28,
                   copy_cal, lambda a: ops.embedding_hip(a[0], a[1]), 2 * 2 ** 28))
 
-    # Copy ceilings: the same kernel as an identity gather (ids 0..n-1, contiguous rows) at
-    # the traffic of the small BASELINE rows, so each row can be read against a plain copy
-    # of its own size in the same run (rope T=4096: 67 MB; embedding T=8192: 134 MB; MLA
-    # T=8192: 52 MB).
+    # Copy ceilings: the library's streaming copy (non-temporal loads and stores, the fastest
+    # copy measured on the box) moving the traffic of the small BASELINE rows, so each row can
+    # be read against a plain copy of its own size in the same run (rope T=4096: 67 MB;
+    # embedding T=8192: 134 MB; MLA T=8192: 52 MB, reads + writes).
     for rows, label in ((4096, "rope T=4096"), (8192, "embedding T=8192"), (3204, "MLA T=8192")):
         def copy_ceil(i, rows=rows):
-            return (torch.arange(rows, device=dev), randn((rows, 4096), bf, 7100 + i))
-        out.append(Op("copy_ceiling", "ceil", f"identity gather [{rows},4096] bf16 (size of {label})",
-                      rows * (8 + 2 * 4096 * 2), copy_ceil, lambda a: ops.embedding_hip(a[0], a[1]),
-                      rows * 4096 * 2))
+            return (randn((rows, 4096), bf, 7100 + i), torch.empty((rows, 4096), dtype=bf, device=dev))
+        out.append(Op("copy_ceiling", "ceil", f"streaming copy [{rows},4096] bf16 (size of {label})",
+                      2 * rows * 4096 * 2, copy_ceil, lambda a: ops.stream_copy_hip(a[0], a[1]), 2 * rows * 4096 * 2))
     return out
 
 

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "ember_silu_and_mul": [_p, _i64, _p, _i64, _i64, _i64, _i32, _p],
     "ember_embedding": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p],
     "ember_gather_rows": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p],
+    "ember_stream_copy": [_p, _p, _i64, _p],
     "ember_scatter_rows2": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p],
     "ember_qk_norm_rope": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _p, _i32, _f32,
                            _p, _p, _i64, _i64, _p, _i64, _i32, _p],

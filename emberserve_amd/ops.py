@@ -238,6 +238,18 @@ def silu_and_mul_hip(x: torch.Tensor, *, out: torch.Tensor | None = None) -> tor
     return out.view(*x.shape[:-1], inter)
 
 
+def stream_copy_hip(src: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out <- src (contiguous, same byte size, 16-byte aligned) with the library's streaming
+    copy: the bandwidth reference of the benchmark's copy-ceiling rows."""
+    _require_device("stream_copy", src, out)
+    nbytes = src.numel() * src.element_size()
+    if (not src.is_contiguous() or not out.is_contiguous() or out.numel() * out.element_size() != nbytes
+            or nbytes % 16 or src.data_ptr() % 16 or out.data_ptr() % 16):
+        raise ValueError("stream_copy: contiguous, 16-byte aligned tensors of one size (a multiple of 16 bytes)")
+    _launch("ember_stream_copy", _lib.load().ember_stream_copy, src.device, src.data_ptr(), out.data_ptr(), nbytes)
+    return out
+
+
 def embedding_hip(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """nn.Embedding forward: out[..., :] = weight[ids[...], :], bit-exact."""
     _require_device("embedding", weight, ids)

@@ -188,6 +188,11 @@ int ember_mla_latent_rope(const void* c, int64_t c_token_stride, int64_t kv_lora
  * [0, src_rows); a negative rows[t] is a padding row, written as zeros; rows[t] >= src_rows
  * writes zeros and sets EMBER_ERR_ROW_INDEX. Rows are row_elems elements of elem_bytes
  * bytes (1, 2, 4 or 8), strides in elements. Bit-exact. */
+/* A streaming copy of `bytes` (a multiple of 16, both pointers 16-byte aligned, no overlap)
+ * with non-temporal loads and stores: the bandwidth reference the benchmark's copy-ceiling
+ * rows measure each op against. No counterpart in the reference. */
+int ember_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
 int ember_gather_rows(const void* src, int64_t src_rows, int64_t src_row_stride,
                       const int64_t* rows, int64_t num_rows,
                       void* dst, int64_t dst_row_stride,
