@@ -44,6 +44,10 @@
 #ifndef EMBER_GU_PACKED_STAGES
 #define EMBER_GU_PACKED_STAGES 3
 #endif
+// 1-16 tokens: x resident in LDS for the whole run (0: per-wave loads from L2).
+#ifndef EMBER_GU_PACKED_XR
+#define EMBER_GU_PACKED_XR 1
+#endif
 // Token tiles up to which the packed kernel loads x per wave from L2 (above: shared in LDS).
 #ifndef EMBER_GU_PACKED_PRIVX_MT
 #define EMBER_GU_PACKED_PRIVX_MT 1
@@ -505,6 +509,85 @@ k_gate_up_silu_packed(GuArgs a) {
   run.merge(last_flags);
 }
 
+// The packed kernel for 1-16 tokens with x resident in LDS. At 16 tokens x (16 x H) no
+// longer fits a CU's L1, so k_gate_up_silu_packed re-reads it from L2 for every slab of its
+// run, in every workgroup: next to the weight stream that is a large share of L2's
+// bandwidth. Here each workgroup loads x once, at the start, in the B-operand fragment order
+// (k32 fragment s at s KiB, lane (n, g): token n, k 32 s + 8 g + [0, 8)), and every unit
+// reads its two fragments from LDS. The same weight ring, units, runs, epilogue and merge
+// as k_gate_up_silu_packed: the same results bit for bit. H <= 32 * kGuXrFrags.
+constexpr int kGuXrFrags = 148;  // 148 KiB of LDS: H <= 4736
+
+template <typename T, int NS>
+__global__ void __launch_bounds__(kGuWaves * kWave, 1)
+k_gate_up_silu_packed_xr(GuArgs a) {
+  using M = GuMfma<T>;
+  using V8 = typename M::v8;
+  constexpr int MT = 1;
+  static_assert(NS >= 2 && NS <= 8, "stages");
+  __shared__ __attribute__((aligned(16))) unsigned char xlds[kGuXrFrags * 1024];
+  __shared__ int last_flags[kGuMaxFlush];
+  const int64_t nk = a.H / kGuBK;
+  const int64_t total = static_cast<int64_t>(a.I / kGuSlab) * nk;
+  const int64_t u0 = gu_start(blockIdx.x, total, gridDim.x);
+  const int nu = static_cast<int>(gu_start(blockIdx.x + 1, total, gridDim.x) - u0);  // >= 1
+  GuRun<T, MT> run(a, u0);
+  const int lane = run.lane, w = run.w, n = run.n, g = run.g;
+
+  // x into LDS first: its loads are the oldest in flight
+  {
+    const T* xl = static_cast<const T*>(a.x) + static_cast<int64_t>(min(n, a.T - 1)) * a.xs + 8 * g;
+    for (int f = w; f < a.H / 32; f += kGuWaves) gu_load_lds16(xl + 32 * f, xlds + f * 1024);
+  }
+  const T* wp = static_cast<const T*>(a.w) + (w * 2 * kWave + lane) * 8;
+  struct Stage {
+    V8 wgt[2], wup[2];
+  };
+  Stage ring[NS];
+  auto issue = [&](Stage& st, int j) {
+    const int t = min(j, nu - 1);  // past the run: repeat its last unit
+    const T* up = wp + gu_packed_pos(blockIdx.x, t, total, gridDim.x) * (2 * kGuWaves * 2 * kWave * 8);
+    constexpr int hs = kGuWaves * 2 * kWave * 8, ps = kWave * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      st.wgt[h] = __builtin_bit_cast(V8, load_stream<T, 8>(up + h * hs));
+      st.wup[h] = __builtin_bit_cast(V8, load_stream<T, 8>(up + h * hs + ps));
+    }
+  };
+  f32x4 acc[MT][2];
+  acc[0][0] = acc[0][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    issue(ring[d], d);
+    __builtin_amdgcn_sched_barrier(0);  // stages issued in ring order, oldest consumed first
+  }
+  // every wave's x loads are done (only the weight stages are left in flight), then visible
+  wait_vm<NS * 4>();
+  gu_barrier();
+  int jk = static_cast<int>(u0 % nk);  // k step of the next unit to compute
+  for (int j0 = 0; j0 < nu; j0 += NS) {
+#pragma unroll
+    for (int d = 0; d < NS; ++d) {
+      const int j = j0 + d;
+      if (j < nu) {  // uniform
+        const unsigned char* xs = xlds + (2 * jk) * 1024 + lane * 16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const V8 xv = *reinterpret_cast<const V8*>(xs + h * 1024);
+          acc[0][0] = M::run(ring[d].wgt[h], xv, acc[0][0]);
+          acc[0][1] = M::run(ring[d].wup[h], xv, acc[0][1]);
+        }
+        if (++jk == nk) jk = 0;
+      }
+      // the same loads on every path (see k_gate_up_silu_packed)
+      issue(ring[d], j + NS);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < nu) run.template end_unit<true>(j, nu, acc);
+    }
+  }
+  run.merge(last_flags);
+}
+
 // The packed kernel for 17-64 tokens. Per unit, every wave needs the x slice of all tokens
 // (MT token tiles, 2 KiB each per 64-k step); loading it per lane from L2, as
 // k_gate_up_silu_packed does, reads 4 copies per unit and stops scaling past 16 tokens
@@ -526,9 +609,11 @@ __global__ void __launch_bounds__(kGuWaves * kWave, 1)
 k_gate_up_silu_packed_x(GuArgs a) {
   using M = GuMfma<T>;
   using V8 = typename M::v8;
-  static_assert(MT % 2 == 0 && MT <= 4, "token tiles");
+  static_assert((MT == 1 || MT % 2 == 0) && MT <= 4, "token tiles");
   static_assert(NS >= 2 && NS <= 4, "stages");
-  constexpr int XF = MT / 2;          // x fragments each wave loads per unit
+  // x fragments each wave loads per unit; with one tile (2 fragments) waves 2 and 3 load
+  // waves 0 and 1's again (identical bytes), so every wave issues the same count
+  constexpr int XF = MT == 1 ? 1 : MT / 2;
   constexpr int LPS = 4 + XF;         // loads per wave per unit
   static_assert(LPS * (NS - 1) < 64, "vmcnt");
   constexpr int XSTAGE = MT * 2 * 1024;
@@ -546,7 +631,7 @@ k_gate_up_silu_packed_x(GuArgs a) {
   int xdst[XF];
 #pragma unroll
   for (int i = 0; i < XF; ++i) {
-    const int f = w + kGuWaves * i;  // fragment 2 mt + h
+    const int f = MT == 1 ? (w & 1) : w + kGuWaves * i;  // fragment 2 mt + h
     const int mt = f >> 1, h = f & 1;
     xsrc[i] = static_cast<const T*>(a.x) + static_cast<int64_t>(min(16 * mt + n, a.T - 1)) * a.xs + 32 * h + 8 * g;
     xdst[i] = f * 1024;
@@ -656,12 +741,29 @@ int launch_gu_packed_x(const GuArgs& a, int64_t programs, hipStream_t st) {
   return launch_status();
 }
 
-// Up to 16 tokens each wave loads its own x (k_gate_up_silu_packed); above, the waves share
-// it through LDS (k_gate_up_silu_packed_x), with the token tiles padded to 2 or 4.
+template <typename T>
+int launch_gu_packed_xr(const GuArgs& a, int64_t programs, hipStream_t st) {
+  hipLaunchKernelGGL((k_gate_up_silu_packed_xr<T, EMBER_GU_PACKED_STAGES>), dim3(static_cast<uint32_t>(programs)),
+                     dim3(kGuWaves * kWave), 0, st, a);
+  return launch_status();
+}
+
+// Up to 16 tokens x stays in LDS for the whole run (k_gate_up_silu_packed_xr; each wave
+// loads its own from L2, k_gate_up_silu_packed, where H is too wide); above, the waves
+// share each unit's x through an LDS ring (k_gate_up_silu_packed_x), with the token tiles
+// padded to 2 or 4.
 template <typename T>
 int launch_gu_packed_typed(const GuArgs& a, int64_t programs, hipStream_t st) {
   const int tiles = (a.T + 15) / 16;
+  // x resident where every run is whole slabs (no partials: measured 30.9 vs 30.5 us at one
+  // token and 33.3 vs 34.7 at 16 for Qwen3-8B over 192 workgroups; 43.8 / 45.6 vs 44.3 / 53.3
+  // for Qwen2.5-7B over 148); with runs that split slabs the per-wave loads measured faster
+  // (Qwen3-8B over 256: 35.4 / 35.6 vs 36.2 / 38.0 us).
+  const bool whole_slabs = (a.I / kGuSlab) % programs == 0;
+  if (tiles <= 1 && EMBER_GU_PACKED_XR && whole_slabs && a.H <= 32 * kGuXrFrags)
+    return launch_gu_packed_xr<T>(a, programs, st);
   if (tiles <= EMBER_GU_PACKED_PRIVX_MT) return launch_gu_packed<T, 1>(a, programs, st);
+  if (tiles <= 1) return launch_gu_packed_x<T, 1>(a, programs, st);
   if (tiles <= 2) return launch_gu_packed_x<T, 2>(a, programs, st);
   if (tiles <= 4) return launch_gu_packed_x<T, 4>(a, programs, st);
   return EMBER_EINVAL;

@@ -99,9 +99,19 @@ class PackedGateUp:
         return self.packed.device
 
 
+def packed_workgroups(inter: int, device: torch.device) -> int:
+    """The default grid of the packed kernels: the most workgroups, up to one per CU, whose
+    runs are whole 64-column slabs (no partial sums to merge), else one per CU. Qwen3-8B (192
+    slabs): 192 workgroups, 30.5 us at one token against 35.4 over 256; Qwen2.5-7B (296
+    slabs): 148, 43.8 against 47.5 us."""
+    slabs, cus = inter // SLAB, gate_up_silu_workgroups(device)
+    per = -(-slabs // cus)
+    return slabs // per if slabs % per == 0 else cus
+
+
 def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> PackedGateUp:
     """The packed copy of weight [2I, H] (fp16/bf16 on the GPU, H and I multiples of 64) for
-    a grid of `num_workgroups` (default: one per CU, the decode kernel's default)."""
+    a grid of `num_workgroups` (default: `packed_workgroups`)."""
     if weight.dim() != 2 or weight.shape[0] % 2 != 0 or weight.dtype not in SUPPORTED_DTYPES:
         raise ValueError(f"pack_gate_up_weight: a [2I, H] fp16/bf16 weight expected, got {tuple(weight.shape)} "
                          f"{weight.dtype}")
@@ -110,7 +120,7 @@ def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> Pa
     I = two_i // 2
     if H % STEP or I % SLAB or weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
         raise ValueError("pack_gate_up_weight: H and I must be multiples of 64, rows unit-stride and 16-byte aligned")
-    programs = gate_up_silu_workgroups(weight.device) if num_workgroups is None else int(num_workgroups)
+    programs = packed_workgroups(I, weight.device) if num_workgroups is None else int(num_workgroups)
     if programs < 1:
         raise ValueError(f"pack_gate_up_weight: num_workgroups must be >= 1, got {programs}")
     packed = torch.empty(two_i * H, dtype=weight.dtype, device=weight.device)

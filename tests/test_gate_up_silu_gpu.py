@@ -175,10 +175,11 @@ def test_pack_weight_matches_the_oracle_permutation(dtype, programs):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("tokens", [1, 7, 16, 17, 33, 40, 64])
-@pytest.mark.parametrize("programs", [7, 256, 300])
+@pytest.mark.parametrize("programs", [7, 19, 76, 256, 300])
 def test_packed_kernel_equals_the_row_kernel(dtype, tokens, programs):
     """Same products in the same order: bit-identical to ember_gate_up_silu (Qwen2.5-0.5B
-    MLP, H 896, I 4864), including runs that split slabs and merge partials."""
+    MLP, H 896, I 4864: 76 slabs), including runs that split slabs and merge partials, and
+    whole-slab runs (19 and 76 workgroups), where up to 16 tokens keep x resident in LDS."""
     from emberserve_amd.gate_up_silu import pack_gate_up_weight
     _say(f"packed gate_up {dtype} T={tokens} G={programs}")
     g = torch.Generator().manual_seed(tokens)
