@@ -387,6 +387,24 @@ def _ops(torch, ops, tables):
         out.append(Op("gate_up_silu_packed", cfg, shape + " (weight packed at load)", nbytes, make_packed,
                       lambda a: gate_up_silu(a[0], a[1], fused=True, packed=a[2]), wbytes))
 
+    def gate_up_prefill(cfg, t, hidden, inter, label):
+        """The dense MLP's gate_up projection + silu_and_mul at prefill token counts: the
+        MFMA GEMM with the activation as its epilogue (64- and 128-column tiles) beside the
+        unfused pair (torch linear = hipBLASLt, then silu_and_mul). Bytes: weights + x + the
+        [T, I] output; the GEMM is MFMA-bound at these sizes (2·T·2I·H flops)."""
+        from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_torch
+        wbytes = 2 * inter * hidden * 2
+
+        def make(i):
+            return (randn((t, hidden), bf, 370 + i), randn((2 * inter, hidden), bf, 380 + i, std=hidden ** -0.5))
+        nbytes = wbytes + t * hidden * 2 + t * inter * 2
+        shape = f"{label}: x[{t},{hidden}] w[{2 * inter},{hidden}] bf16"
+        for tile in (64, 128):
+            out.append(Op("gate_up_silu_gemm", cfg, shape + f" (MFMA GEMM, {tile}+{tile}-column tiles)", nbytes, make,
+                          lambda a, tile=tile: gate_up_silu_gemm(a[0], a[1], column_tile=tile), wbytes + t * hidden * 2))
+        out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
+                      lambda a: gate_up_silu_torch(a[0], a[1]), wbytes + t * hidden * 2))
+
     def moe_gate_up(cfg, n):
         """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's
         geometry (H 2048, I 1408, 64 experts, top-6), decode batch n: bytes are the used
@@ -476,6 +494,9 @@ def _ops(torch, ops, tables):
     for t in (1, 16):
         gate_up("mlp", t, 4096, 12288, "qwen3-8b")
         gate_up("mlp", t, 3584, 18944, "qwen2.5-7b")
+    for t in (256, 8192):
+        gate_up_prefill("mlp_prefill", t, 4096, 12288, "qwen3-8b")
+        gate_up_prefill("mlp_prefill", t, 3584, 18944, "qwen2.5-7b")
     for n in (1, 8, 64):
         moe_gate_up("moe", n)
     for n in (1, 64, 8192):

@@ -1,0 +1,288 @@
+// Prefill-size gate_up projection with silu_and_mul as its epilogue, for gfx950:
+//   out[t, j] = round(round(silu(g)) * u),  g = round(x[t] . W[j]),  u = round(x[t] . W[I + j])
+// for t < T, j < I, with W [2I, H] the nn.Linear(H, 2I) weight (gate rows, then up rows).
+//
+// Reference: Qwen2MLP.forward, emberserve/model/qwen2.py:60-61 (gate_up_proj, then
+// ops.silu_and_mul), where the [T, 2I] projection is written and read back. Here it never
+// leaves the chip: each workgroup computes a 256-token x (BNG gate + BNG up) column tile with
+// bf16/fp16 MFMA (v_mfma_f32_16x16x32) and writes only the [256, BNG] activation tile.
+//
+// Structure:
+//   * 8 waves: wave (grp, q) owns tokens 64 q .. 64 q + 63 of the tile and columns
+//     BNG/2 grp .. BNG/2 grp + BNG/2 - 1 of both the gate and the up half, so it holds
+//     (BNG / 16) x 4 accumulator tiles of 16 x 16;
+//   * the tile's operands stream through an LDS ring of "double stages" of 64 k (three for
+//     the 64-column tile, two for the 128-column one, which fill 128 KiB): rows of 128
+//     bytes (one 64-k line per row), so each direct-to-LDS load (global_load_lds_dwordx4)
+//     moves 8 rows x 128 B; 16-byte chunks XOR-swizzled by row & 7 so the fragment reads
+//     (one row per lane) spread over the banks. At 256 tokens each workgroup streams its
+//     weight rows from HBM once, and the third buffer (two double stages in flight) took the
+//     Qwen3-8B call from 91.7 to 70.0 us;
+//   * ping-pong: the two waves of each SIMD belong to different groups (grp), and group 1
+//     starts one barrier late, so between two barriers one group reads fragments and issues
+//     loads while the other runs its MFMAs;
+//   * XCD-aware tile order: consecutive workgroups land on different XCDs (round robin), so
+//     the order is remapped to give each XCD a contiguous range of tiles, grouped GROUP_M
+//     token tiles at a time over a band of column tiles (their weight rows stay in that
+//     XCD's L2).
+// The k order of every accumulator is the decode kernels' (32-k steps in order, one chain),
+// so a token's result is bit-identical to ember_gate_up_silu_packed over whole-slab runs.
+// The epilogue is the decode kernels' exact one (expf and a division); v_exp_f32 / v_rcp_f32
+// measured 3% faster at 8192 tokens and would give up that identity.
+//
+// Measured on MI355X (bf16, µs; this kernel at the better column tile / hipBLASLt +
+// silu_and_mul): Qwen3-8B 256 tokens 70.0 / 72.6, 8192 tokens 1286 / 1235; Qwen2.5-7B 256
+// tokens 110 / 88.5, 8192 tokens 1791 / 1834. The library therefore keeps the unfused pair
+// by default at these sizes and runs this kernel when the fused form is asked for.
+#include "ember_common.h"
+
+#ifndef EMBER_GEMM_GROUP_M
+#define EMBER_GEMM_GROUP_M 8
+#endif
+// Double-stage buffers of the 64-column tile (the 128-column tile's two fill 128 KiB).
+#ifndef EMBER_GEMM_NBUF64
+#define EMBER_GEMM_NBUF64 3
+#endif
+
+namespace ember {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct GemmMfma;
+template <>
+struct GemmMfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct GemmMfma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kGemmBM = 256;  // tokens per tile
+constexpr int kGemmRowB = 128;  // LDS row: 64 k of one operand row
+
+__device__ __forceinline__ void gemm_load_lds16(const void* gptr, void* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)(
+                                             reinterpret_cast<uintptr_t>(lds_base)), 16, 0, 0);
+#else
+  (void)gptr;
+  (void)lds_base;
+#endif
+}
+
+// s_waitcnt vmcnt(N) / lgkmcnt(0) alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void gemm_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void gemm_wait_vm0() { gemm_wait_vm<0>(); }
+__device__ __forceinline__ void gemm_wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
+
+// A workgroup barrier with no fence (the waits above are explicit); the asm clobbers keep
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void gemm_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+struct GemmArgs {
+  const void* x;
+  int64_t xs;
+  const void* w;
+  int64_t ws;
+  void* out;
+  int64_t os;
+  int T, H, I;
+};
+
+template <typename T, int BNG>
+__global__ void __launch_bounds__(512, 1)
+k_gate_up_silu_gemm(GemmArgs a) {
+  using M = GemmMfma<T>;
+  using V8 = typename M::v8;
+  static_assert(BNG == 64 || BNG == 128, "column tile");
+  constexpr int NT = BNG / 16;                 // row tiles per wave: NT / 2 gate, NT / 2 up
+  constexpr int WREG = 2 * BNG * kGemmRowB;    // weight region of a double stage
+  constexpr int XREG = kGemmBM * kGemmRowB;    // x region
+  constexpr int DST = WREG + XREG;             // one double stage (64 k)
+  constexpr int LOADS = (2 * BNG + kGemmBM) / 8 / 8;  // 1 KiB load instructions per wave per double stage
+  // Double-stage buffers: NBUF - 1 double stages of loads in flight while one is consumed.
+  constexpr int NBUF = BNG == 64 ? EMBER_GEMM_NBUF64 : 2;
+  static_assert(NBUF * DST <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[NBUF * DST];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = w >> 2;
+  const int q = w & 3;
+  const int n = lane & 15, g = lane >> 4;
+
+  // XCD-aware tile order, then GROUP_M token tiles per band of column tiles
+  const int mtiles = (a.T + kGemmBM - 1) / kGemmBM;
+  const int ntiles = a.I / BNG;
+  int pid = blockIdx.x;
+  {
+    const int nb = gridDim.x;
+    const int per = (nb + 7) / 8;
+    const int xcd = pid % 8, idx = pid / 8;
+    const int full = nb % 8 == 0 ? 8 : nb % 8;
+    pid = xcd < full ? xcd * per + idx : full * per + (xcd - full) * (per - 1) + idx;
+  }
+  constexpr int GM = EMBER_GEMM_GROUP_M;
+  const int group = pid / (GM * ntiles);
+  const int first_m = group * GM;
+  const int gsize = min(mtiles - first_m, GM);
+  const int mt = first_m + (pid % (GM * ntiles)) % gsize;
+  const int nt = (pid % (GM * ntiles)) / gsize;
+  const int m0 = mt * kGemmBM, n0 = nt * BNG;
+
+  const T* X = static_cast<const T*>(a.x);
+  const T* W = static_cast<const T*>(a.w);
+  // This wave's load instructions of a double stage: instruction ins moves rows
+  // 8 (ins % 32) + lane / 8 of region ins / 32-ish (weight rows first, then x rows); lane l
+  // loads 16-byte chunk (l % 8) ^ (row % 8) of its row into slot l of the 1 KiB block.
+  const T* src[LOADS];
+  int dst[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int ins = LOADS * w + i;  // 0 .. 2 BNG / 8 + 31
+    const int row = 8 * ins + (lane >> 3);
+    const int c = (lane & 7) ^ (row & 7);
+    if (row < 2 * BNG) {
+      const int wr = row < BNG ? n0 + row : a.I + n0 + (row - BNG);
+      src[i] = W + static_cast<int64_t>(wr) * a.ws + 8 * c;
+    } else {
+      const int xr = row - 2 * BNG;
+      src[i] = X + static_cast<int64_t>(min(m0 + xr, a.T - 1)) * a.xs + 8 * c;  // padded tokens: the last real one
+    }
+    dst[i] = ins * 1024;  // the weight region is rows 0 .. 2 BNG - 1, the x region follows
+  }
+  const int nd = a.H / 64;  // double stages
+  auto issue = [&](int d) {
+    const int kk = min(d, nd - 1) * 64;
+    unsigned char* st = lds + (d % NBUF) * DST;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) gemm_load_lds16(src[i] + kk, st + dst[i]);
+  };
+  int woff[NT], xoff[4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    woff[t] = ((t < NT / 2 ? 0 : BNG) + (BNG / 2) * grp + 16 * (t % (NT / 2)) + n) * kGemmRowB;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) xoff[u] = WREG + (64 * q + 16 * u + n) * kGemmRowB;
+  const int sw = n & 7;  // row % 8 of every fragment row
+
+  f32x4 acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  V8 fw[NT], fx[4];
+
+#pragma unroll
+  for (int d = 0; d < NBUF - 1; ++d) issue(d);
+  gemm_wait_vm<(NBUF - 2) * LOADS>();
+  gemm_barrier();
+  // M(s): at an even 32-k stage issue the next double stage's loads into the other buffer;
+  // read this stage's fragments; at an odd stage wait for the next double stage's loads.
+  auto mphase = [&](int s, bool even) {
+    if (even) issue(s / 2 + NBUF - 1);
+    const unsigned char* st = lds + ((s >> 1) % NBUF) * DST;
+    const int co = ((4 * (s & 1) + g) ^ sw) << 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) fw[t] = *reinterpret_cast<const V8*>(st + woff[t] + co);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fx[u] = *reinterpret_cast<const V8*>(st + xoff[u] + co);
+    if (!even) gemm_wait_vm<(NBUF - 2) * LOADS>();  // the next double stage has landed
+    gemm_wait_lgkm0();
+  };
+  auto cphase = [&]() {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[t][u] = M::run(fw[t], fx[u], acc[t][u]);
+  };
+  const int nk = 2 * nd;
+  if (grp == 1) gemm_barrier();
+  for (int s = 0; s < nk; s += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mphase(s + h, h == 0);
+      gemm_barrier();
+      cphase();
+      gemm_barrier();
+    }
+  }
+  if (grp == 0) gemm_barrier();
+  gemm_wait_vm0();
+
+  // Epilogue: lane (n, g) holds rows 4g + r of each 16-row tile for token 16 u + n.
+  T* out = static_cast<T*>(a.out);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int tok = m0 + 64 * q + 16 * u + n;
+    if (tok < a.T) {
+#pragma unroll
+      for (int t = 0; t < NT / 2; ++t) {
+        const int col = n0 + (BNG / 2) * grp + 16 * t + 4 * g;
+        Pack<T, 4> o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gf = round_to<T>(acc[t][u][r]);
+          const float uf = round_to<T>(acc[t + NT / 2][u][r]);
+          const float act = round_to<T>(gf / (1.0f + expf(-gf)));
+          o.v[r] = from_f32<T>(act * uf);
+        }
+        store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
+      }
+    }
+  }
+}
+
+template <typename T, int BNG>
+int launch_gemm(const GemmArgs& a, hipStream_t st) {
+  const int64_t grid = cdiv(a.T, kGemmBM) * (a.I / BNG);
+  if (grid > 0x7fffffffLL) return EMBER_EINVAL;
+  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+                                       int dtype, int64_t tokens, int64_t hidden, int64_t inter,
+                                       int64_t column_tile, void* out, int64_t out_row_stride, void* stream) {
+  using namespace ember;
+  if (tokens == 0) return EMBER_OK;
+  if (tokens < 0 || tokens > (int64_t(1) << 24) || hidden < 64 || hidden % 64 != 0 || hidden > (int64_t(1) << 20) ||
+      (column_tile != 64 && column_tile != 128) || inter < column_tile || inter % column_tile != 0 ||
+      inter > (int64_t(1) << 28))
+    return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || w == nullptr || out == nullptr || !aligned16(x) || !aligned16(w) || !aligned16(out))
+    return EMBER_EINVAL;
+  if (x_row_stride < hidden || w_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 ||
+      w_row_stride % 8 != 0 || out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(tokens),
+             static_cast<int>(hidden), static_cast<int>(inter)};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16)
+    return column_tile == 64 ? launch_gemm<_Float16, 64>(a, st) : launch_gemm<_Float16, 128>(a, st);
+  return column_tile == 64 ? launch_gemm<__bf16, 64>(a, st) : launch_gemm<__bf16, 128>(a, st);
+}

@@ -14,8 +14,9 @@ Dispatch: by default the kernel runs for up to FUSED_TOKENS tokens, where it mea
 faster than the unfused pair (torch's linear, i.e. hipBLASLt, then this library's
 silu_and_mul) on MI355X: Qwen3-8B (H 4096, I 12288) 40 vs 45 us at 1-16 tokens, Qwen2.5-7B
 (H 3584, I 18944) 54.5 vs 54.8 us. From 32 tokens on the library GEMM was as fast or faster,
-so the unfused pair runs there; `fused=True` forces the kernel (up to 64 tokens) and
-`fused=False` the pair. Over a weight packed at load time (`packed=`) the kernel runs by
+so the unfused pair runs there; `fused=True` forces the kernel (up to 64 tokens; above, the
+prefill-size MFMA GEMM with the activation as its epilogue, `gate_up_silu_gemm`, which also
+never materialises the [T, 2I] projection) and `fused=False` the pair. Over a weight packed at load time (`packed=`) the kernel runs by
 default up to PACKED_FUSED_TOKENS: 35.3 vs 46.1 us at 16 tokens and 37.1 vs 45.8 at 32
 (Qwen3-8B), 52.0 vs 56.7 at 32 (Qwen2.5-7B); at 48-64 tokens it is ahead at Qwen3-8B
 (44.5 vs 47.8) and behind at Qwen2.5-7B (65.0 vs 63.0). Where the kernel does not apply (more than 64 tokens, fp32, shapes
@@ -43,6 +44,9 @@ MAX_TOKENS = 64           # the kernels' limit
 PACKED_MAX_TOKENS = 64
 FUSED_TOKENS = 16         # default dispatch, row kernel: the kernel up to here, the pair above
 PACKED_FUSED_TOKENS = 32  # default dispatch over a packed weight
+# Prefill sizes (gate_up_silu_gemm): 64 + 64-column tiles up to this many tokens (more
+# workgroups on a short token range), 128 + 128 above (fewer re-reads of x).
+GEMM_TILE_SMALL, GEMM_TILE_LARGE, GEMM_SMALL_TILE_TOKENS = 64, 128, 512
 SLAB = 64          # output columns per workgroup
 STEP = 64          # k per pipeline stage
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
@@ -129,6 +133,30 @@ def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> Pa
     return PackedGateUp(packed, H, I, programs)
 
 
+def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128) -> Tensor:
+    """silu_and_mul(F.linear(x, weight)) as one MFMA GEMM whose epilogue applies the
+    activation (`ember_gate_up_silu_gemm`): 256-token x (column_tile gate + column_tile up)
+    tiles, any token count. Needs fp16/bf16, H a multiple of 64, I of column_tile."""
+    if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
+        raise ValueError(f"gate_up_silu_gemm: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
+                         "a [2I, H] gate_up projection")
+    _require_device("gate_up_silu_gemm", x, weight)
+    H = x.shape[-1]
+    I = weight.shape[0] // 2
+    x2 = x.reshape(-1, H)
+    T = x2.shape[0]
+    out = torch.empty((T, I), dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out.view(*x.shape[:-1], I)
+    if not (_fits(x2, weight, out, max_tokens=1 << 24) and I % column_tile == 0):
+        raise ValueError(f"gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {I}, "
+                         f"column_tile {column_tile}, {x.dtype})")
+    _launch("ember_gate_up_silu_gemm", _lib.load().ember_gate_up_silu_gemm, x.device,
+            x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
+            T, H, I, column_tile, out.data_ptr(), out.stride(0))
+    return out.view(*x.shape[:-1], I)
+
+
 def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None,
                  fused: bool | None = None, packed: PackedGateUp | None = None) -> Tensor:
     """silu_and_mul(F.linear(x, weight)) with weight [2I, H] (qwen2.py:60-61). With `packed`
@@ -147,6 +175,10 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     if T == 0:
         return out.view(*x.shape[:-1], I)
     limit, default = (PACKED_MAX_TOKENS, PACKED_FUSED_TOKENS) if packed is not None else (MAX_TOKENS, FUSED_TOKENS)
+    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and I % GEMM_TILE_SMALL == 0:
+        # the fused form asked for at prefill sizes: the MFMA GEMM with the activation epilogue
+        tile = GEMM_TILE_SMALL if T <= GEMM_SMALL_TILE_TOKENS or I % GEMM_TILE_LARGE else GEMM_TILE_LARGE
+        return gate_up_silu_gemm(x, weight, column_tile=tile)
     if fused is False or (fused is None and T > default) or not _fits(x2, weight, out, limit):
         return gate_up_silu_torch(x, weight)
     programs = gate_up_silu_workgroups(x.device) if num_workgroups is None else int(num_workgroups)

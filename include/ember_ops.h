@@ -426,6 +426,18 @@ int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t n
                                   int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
                                   int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
 
+/* The gate_up projection + silu_and_mul at prefill sizes: an MFMA GEMM over 256-token x
+ * (column_tile gate + column_tile up) tiles whose epilogue applies silu_and_mul, writing only
+ * out [tokens, inter] (out[t, j] = round(round(silu(g)) * u), g and u the dot products
+ * rounded to the dtype). x [tokens, hidden], w [2 inter, hidden] (gate rows, then up rows),
+ * fp16 or bf16, 16-byte aligned, unit inner stride; hidden a multiple of 64, inter of
+ * column_tile (64 or 128). No workspace. Each accumulator runs over k in order in one chain,
+ * so a token's result equals ember_gate_up_silu_packed's over whole-slab runs bit for bit.
+ * Replaces qwen2.py:60-61 (gate_up_proj, then silu_and_mul) without the [T, 2I] round trip. */
+int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
+                            int64_t tokens, int64_t hidden, int64_t inter, int64_t column_tile, void* out,
+                            int64_t out_row_stride, void* stream);
+
 /* Rearranges a gate_up weight W [2I, H] (row stride w_row_stride elements, fp16 or bf16,
  * 16-byte aligned) into the layout ember_gate_up_silu_packed reads with num_workgroups
  * workgroups: 2 I H elements in units of 8192. Unit (slab, j) (slab < I / 64, j < H / 64) is

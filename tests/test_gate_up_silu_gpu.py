@@ -231,3 +231,57 @@ def test_swiglu_mlp_packed_weights():
         changed = mlp(x)
         assert mlp._packed is None
         assert torch.equal(changed, mlp.down_proj(gate_up_silu(x, mlp.gate_up_proj.weight)))
+
+
+# ---- prefill sizes: the MFMA GEMM with the activation as its epilogue ----
+@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("tokens", [1, 16, 64, 300])
+def test_gemm_equals_the_packed_kernel(tile, tokens):
+    """Every accumulator runs over k in order in one chain, as the packed kernel's over
+    whole-slab runs (76 workgroups for Qwen2.5-0.5B's 76 slabs): bit-identical per token,
+    in 64-token chunks past 64 (token tiles padded, a partial last tile)."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm, pack_gate_up_weight
+    _say(f"gemm gate_up tile={tile} T={tokens}")
+    g = torch.Generator().manual_seed(900 + tokens)
+    x = (torch.randn(tokens, 896, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(2 * 4864, 896, generator=g) / 896 ** 0.5).to(torch.bfloat16).to(DEV)
+    got = gate_up_silu_gemm(x, w, column_tile=tile)
+    packed = pack_gate_up_weight(w, 76)
+    for t0 in range(0, tokens, 64):
+        want = gate_up_silu(x[t0:t0 + 64], w, fused=True, packed=packed)
+        assert torch.equal(got[t0:t0 + 64].view(torch.int16), want.view(torch.int16)), t0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens", [256, 777])
+def test_gemm_against_oracle(dtype, tokens):
+    """Qwen3-8B MLP shape (H 4096, I 12288) on sampled columns against the oracle."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm
+    _say(f"gemm gate_up oracle {dtype} T={tokens}")
+    g = torch.Generator().manual_seed(950 + tokens)
+    x = (torch.randn(tokens, 4096, generator=g) * 0.5).to(dtype)
+    w = (torch.randn(2 * 12288, 4096, generator=g) / 64).to(dtype)
+    got = gate_up_silu_gemm(x.to(DEV), w.to(DEV), column_tile=128).cpu()
+    cols = torch.randperm(12288, generator=g)[:128]
+    rows = torch.randperm(tokens, generator=g)[:64]
+    _check(got[rows][:, cols], x[rows], torch.cat([w[cols], w[12288 + cols]]), f"gemm T={tokens}")
+
+
+def test_gemm_rejects_bad_tiles():
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm
+    x = torch.randn(4, 128, device=DEV).to(torch.bfloat16)
+    w = torch.randn(2 * 96, 128, device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        gate_up_silu_gemm(x, w, column_tile=64)  # I = 96 is not a multiple of 64
+
+
+def test_fused_true_past_64_tokens_runs_the_gemm():
+    """gate_up_silu(..., fused=True) above the decode kernels' limit is the GEMM (64-column
+    tiles up to 512 tokens, 128 above); the default keeps the unfused pair."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm
+    g = torch.Generator().manual_seed(77)
+    w = (torch.randn(2 * 256, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
+    for tokens, tile in ((100, 64), (600, 128)):
+        x = (torch.randn(tokens, 512, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+        assert torch.equal(gate_up_silu(x, w, fused=True), gate_up_silu_gemm(x, w, column_tile=tile))
+        assert torch.equal(gate_up_silu(x, w), gate_up_silu_torch(x, w))
