@@ -1008,19 +1008,27 @@ k_moe_gate_up_silu(MoeGuArgs a) {
 // time, each load instruction moves 1 KiB of consecutive lanes, and the ring is in registers,
 // so no LDS limits how many workgroups share a CU. Same grid, products, order and epilogue
 // as k_moe_gate_up_silu: bit-identical results.
-template <typename T, int NS>
-__global__ void __launch_bounds__(kGuWaves * kWave)
+//
+// WPB = 2 (one k split only): a workgroup of two waves covers half a slab (waves 2 hs and
+// 2 hs + 1 of the slab's layout, hs = the grid's slab index % 2), so a small batch's
+// (block, slab) pairs become twice as many workgroups without a k split to merge. Measured
+// at Moonlight's geometry, one token (6 used blocks x 22 slabs): see moe_half_slabs.
+template <typename T, int NS, int WPB>
+__global__ void __launch_bounds__(WPB * kWave)
 k_moe_gate_up_silu_packed(MoeGuArgs a) {
   using M = GuMfma<T>;
   using V8 = typename M::v8;
   static_assert(NS >= 2 && NS <= 8, "stages");
-  const MoeTile tile = moe_tile();
+  static_assert(WPB == 4 || WPB == 2, "waves per workgroup");
+  MoeTile tile = moe_tile();
   const int blk = tile.blk;
   const int e = a.block_expert[blk];  // uniform (scalar load)
   if (e < 0 || e >= a.E) return;
+  // the wave's place in its 64-column slab
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6) + (WPB == 2 ? 2 * (tile.slab & 1) : 0));
+  if (WPB == 2) tile.slab >>= 1;
   const int slab = tile.slab;
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
   const int nk = a.kc / kGuBK;
@@ -1345,8 +1353,9 @@ int ember_moe_gate_up_silu_pack_weight(const void* w, int64_t w_expert_stride, i
 int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
                                   int dtype, int64_t num_experts, int64_t hidden, int64_t inter,
                                   const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
-                                  int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
-                                  int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream) {
+                                  int64_t num_valid, int64_t top_k, int64_t num_splits, int64_t half_slabs,
+                                  void* workspace, int64_t workspace_bytes, void* out, int64_t out_row_stride,
+                                  void* stream) {
   if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
   MoeGuArgs a{};
   const int rc = moe_setup(a, x, x_row_stride, num_tokens, packed_w, 0, 0, true, dtype, num_experts, hidden, inter,
@@ -1355,12 +1364,24 @@ int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t n
   if (rc != EMBER_OK) return rc;
   const dim3 grid = moe_grid(num_blocks, inter, num_splits);
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (half_slabs != 0 && half_slabs != 1) return EMBER_EINVAL;
+  if (half_slabs && num_splits != 1) return EMBER_EINVAL;
+  if (half_slabs) {
+    const dim3 hgrid(static_cast<uint32_t>(2 * (inter / kGuSlab)), 1u, static_cast<uint32_t>(num_blocks));
+    if (dtype == EMBER_F16)
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES, 2>), hgrid, dim3(2 * kWave), 0,
+                         st, a);
+    else
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES, 2>), hgrid, dim3(2 * kWave), 0,
+                         st, a);
+    return launch_status();
+  }
   if (dtype == EMBER_F16) {
-    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES>), grid, dim3(kGuWaves * kWave), 0,
-                       st, a);
+    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES, 4>), grid,
+                       dim3(kGuWaves * kWave), 0, st, a);
   } else {
-    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES>), grid, dim3(kGuWaves * kWave), 0,
-                       st, a);
+    hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES, 4>), grid, dim3(kGuWaves * kWave),
+                       0, st, a);
   }
   return launch_status();
 }

@@ -99,6 +99,15 @@ def moe_num_splits(num_valid: int, num_experts: int, hidden: int, inter: int, de
     return 1 if _busy(num_valid, num_experts, inter) < num_sms(device) else 2
 
 
+def moe_half_slabs(num_valid: int, num_experts: int, inter: int, device: torch.device) -> bool:
+    """Packed weights, one split: two-wave half-slab workgroups while the four-wave ones
+    (used blocks x slabs) number from one to 1.5 times the CUs. Measured at Moonlight's
+    geometry (µs, four-wave / half-slab): 1 token 15.3 / 15.9, 2 tokens 32.3 / 28.8 (30.2 at
+    the best split), 3 tokens 34.4 / 32.5, 4 tokens 40.1 / 41.3, 8 tokens 57.6 / 60.7."""
+    busy, cus = _busy(num_valid, num_experts, inter), num_sms(device)
+    return cus <= busy < 1.5 * cus
+
+
 def _workspace_bytes(splits: int, num_valid: int, inter: int, num_blocks: int) -> int:
     return _lib.load().ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, splits)
 
@@ -163,11 +172,13 @@ def pack_moe_gate_up_weight(w_gate_up: Tensor) -> PackedExperts:
 
 
 def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
-                     top_k: int, *, num_splits: int | None = None, packed: PackedExperts | None = None) -> Tensor:
+                     top_k: int, *, num_splits: int | None = None, packed: PackedExperts | None = None,
+                     half_slabs: bool | None = None) -> Tensor:
     """act [num_valid, I]: act[id] = silu_and_mul(x[id // top_k] @ w_gate_up[e].T) for every
     assignment id in a block of expert e (moe_triton.py:339-340, fused). With `packed`
     (`pack_moe_gate_up_weight(w_gate_up)`), the kernel reads the packed copy instead (the same
-    bits)."""
+    bits); `half_slabs` (packed, one split; default `moe_half_slabs`) runs it over two-wave
+    workgroups of 32 columns."""
     assert x.dim() == 2 and w_gate_up.dim() == 3 and w_gate_up.shape[2] == x.shape[1], (x.shape, w_gate_up.shape)
     assert w_gate_up.shape[1] % 2 == 0
     assert sorted_ids.dtype == torch.int32 and block_expert.dtype == torch.int32
@@ -203,10 +214,14 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
                           x.device)
     ws_ptr, ws_bytes = (ws.data_ptr(), ws.numel() * 4) if ws is not None else (None, 0)
     if packed is not None:
+        if half_slabs is None:
+            half_slabs = num_splits == 1 and moe_half_slabs(num_valid, E, inter, x.device)
+        if half_slabs and num_splits != 1:
+            raise ValueError("moe_gate_up_silu: half_slabs needs one k split")
         _launch("ember_moe_gate_up_silu_packed", _lib.load().ember_moe_gate_up_silu_packed, x.device,
                 x.data_ptr(), x.stride(0), x.shape[0], packed.packed.data_ptr(), _lib.dtype_tag(x.dtype), E, H, inter,
                 sorted_ids.data_ptr(), block_expert.data_ptr(), block_expert.numel(), num_valid, top_k, num_splits,
-                ws_ptr, ws_bytes, out.data_ptr(), out.stride(0))
+                int(bool(half_slabs)), ws_ptr, ws_bytes, out.data_ptr(), out.stride(0))
     else:
         _launch("ember_moe_gate_up_silu", _lib.load().ember_moe_gate_up_silu, x.device,
                 x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),

@@ -419,12 +419,15 @@ int ember_moe_gate_up_silu_pack_weight(const void* w, int64_t w_expert_stride, i
 /* ember_moe_gate_up_silu over weights packed by ember_moe_gate_up_silu_pack_weight: the same
  * arguments less the weight strides, the same workspace, limits and errors, and the same
  * results bit for bit (the same products in the same order); replaces the same reference
- * calls (moe_triton.py:332-345). */
+ * calls (moe_triton.py:332-345). half_slabs = 1 (one split only) runs two-wave workgroups
+ * over 32 output columns each instead of four-wave ones over 64: twice the workgroups,
+ * for batches whose used blocks x slabs leave CUs idle. */
 int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
                                   int dtype, int64_t num_experts, int64_t hidden, int64_t inter,
                                   const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
-                                  int64_t num_valid, int64_t top_k, int64_t num_splits, void* workspace,
-                                  int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+                                  int64_t num_valid, int64_t top_k, int64_t num_splits, int64_t half_slabs,
+                                  void* workspace, int64_t workspace_bytes, void* out, int64_t out_row_stride,
+                                  void* stream);
 
 /* The gate_up projection + silu_and_mul at prefill sizes: an MFMA GEMM over 256-token x
  * (column_tile gate + column_tile up) tiles whose epilogue applies silu_and_mul, writing only

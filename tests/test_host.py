@@ -426,6 +426,12 @@ def test_moe_split_rule_and_workspace(monkeypatch):
     # packed kernel: one split
     assert moe.moe_num_splits(6, 64, 2048, 1408, dev, packed=True) == 1
     assert moe.moe_num_splits(12, 64, 2048, 1408, dev, packed=True) == 1
+    # packed, half-slab workgroups: from one to 1.5 times the CUs of four-wave ones
+    assert not moe.moe_half_slabs(6, 64, 1408, dev)    # 132
+    assert moe.moe_half_slabs(12, 64, 1408, dev)       # 264
+    assert moe.moe_half_slabs(17, 64, 1408, dev)       # 374 < 384
+    assert not moe.moe_half_slabs(18, 64, 1408, dev)   # 396
+    assert not moe.moe_half_slabs(24, 64, 1408, dev)   # 528
     assert moe.moe_num_splits(12, 64, 64 * 3, 1408, dev) == 1  # three k steps: no even split
     lib = _lib.load()
     assert lib.ember_moe_gate_up_silu_workspace_bytes(6, 1408, 61, 1) == 0

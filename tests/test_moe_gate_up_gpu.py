@@ -139,3 +139,18 @@ def test_moe_packed_bad_assignment_sets_error_bit():
     moe_gate_up_silu(x[:2].to(DEV), dw, sorted_ids, block_expert, nv, K, packed=pack_moe_gate_up_weight(dw))
     torch.cuda.synchronize()
     assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX
+
+
+@pytest.mark.parametrize("n", [1, 3, 37])
+def test_moe_packed_half_slabs_equal_full_slabs(n):
+    """Two-wave workgroups over 32 columns run every wave's rows over the whole k range as the
+    four-wave ones do: bit-identical (one split)."""
+    x, w, ids = _inputs(n, torch.bfloat16, seed=300 + n)
+    dx, dw = x.to(DEV), w.to(DEV)
+    packed = pack_moe_gate_up_weight(dw)
+    sorted_ids, block_expert, nv = moe_align(ids.to(DEV), E)
+    a = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=1, packed=packed, half_slabs=False)
+    b = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=1, packed=packed, half_slabs=True)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    with pytest.raises(ValueError):
+        moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=2, packed=packed, half_slabs=True)
