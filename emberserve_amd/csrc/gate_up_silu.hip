@@ -833,6 +833,8 @@ struct MoeGuArgs {
   int64_t os;
   const int32_t* sorted_ids;
   const int32_t* block_expert;
+  const void* topk;   // direct mode (no alignment): assignment ids' experts; null otherwise
+  int id_bytes;       // 4 or 8 (topk)
   int E, H, I, num_valid, a_div;
   int kc;             // k per split
   float* part;        // [splits][num_valid][2I] fp32 partials (splits > 1)
@@ -858,12 +860,10 @@ __device__ __forceinline__ MoeTile moe_tile() {
 
 template <typename T>
 __device__ __forceinline__ void moe_finish(const MoeGuArgs& a, f32x4 (&acc)[2], const MoeTile& tile, int w,
-                                           int lane) {
+                                           int lane, int id) {
   const int blk = tile.blk, slab = tile.slab;
-  const int n = lane & 15;
   const int g = lane >> 4;
-  // lane (n, g): assignment n of the block, output columns slab * 64 + 16 w + 4g + [0, 4)
-  const int id = a.sorted_ids[blk * 16 + n];
+  // lane (n, g): assignment id (slot n of the block), output columns slab * 64 + 16 w + 4g + [0, 4)
   const bool mine = id >= 0 && id < a.num_valid;
   const int64_t col = static_cast<int64_t>(slab) * kGuSlab + w * kGuRows + 4 * g;
   const int splits = tile.splits;
@@ -997,7 +997,7 @@ k_moe_gate_up_silu(MoeGuArgs a) {
     if (j + NS - 1 < nk) issue(j + NS - 1);
     compute(j);
   }
-  moe_finish<T>(a, acc, tile, w, lane);
+  moe_finish<T>(a, acc, tile, w, lane, a.sorted_ids[tile.blk * 16 + (lane & 15)]);
 }
 
 
@@ -1022,23 +1022,38 @@ k_moe_gate_up_silu_packed(MoeGuArgs a) {
   static_assert(WPB == 4 || WPB == 2, "waves per workgroup");
   MoeTile tile = moe_tile();
   const int blk = tile.blk;
-  const int e = a.block_expert[blk];  // uniform (scalar load)
-  if (e < 0 || e >= a.E) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  // Direct mode: "block" blk is assignment blk alone, in lane 0 (the other 15 lanes are
+  // padding on the same token's row); its expert is read from the routing ids themselves.
+  const bool direct = a.topk != nullptr;  // uniform
+  int e, id;
+  if (direct) {
+    e = a.id_bytes == 8 ? static_cast<int>(static_cast<const int64_t*>(a.topk)[blk])
+                        : static_cast<const int32_t*>(a.topk)[blk];
+    const int64_t e64 = a.id_bytes == 8 ? static_cast<const int64_t*>(a.topk)[blk] : e;
+    if (e64 < 0 || e64 >= a.E) {  // dropped, as moe_align drops it
+      if (threadIdx.x == 0 && tile.slab == 0) atomicOr(a.err, EMBER_ERR_EXPERT_ID);
+      return;
+    }
+    id = n == 0 ? blk : a.num_valid;
+  } else {
+    e = a.block_expert[blk];  // uniform (scalar load)
+    if (e < 0 || e >= a.E) return;
+    id = a.sorted_ids[blk * 16 + n];
+  }
   // the wave's place in its 64-column slab
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6) + (WPB == 2 ? 2 * (tile.slab & 1) : 0));
   if (WPB == 2) tile.slab >>= 1;
   const int slab = tile.slab;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int n = lane & 15;
-  const int g = lane >> 4;
   const int nk = a.kc / kGuBK;
   const int slabs = a.I / kGuSlab;
   constexpr int kUnit = 2 * kGuWaves * 2 * kWave * 8;  // elements
   const T* wp = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes +
                 (static_cast<int64_t>(tile.split) * nk * slabs + slab) * kUnit + (w * 2 * kWave + lane) * 8;
   const int64_t ustride = static_cast<int64_t>(slabs) * kUnit;
-  const int id = a.sorted_ids[blk * 16 + n];
-  int64_t row = id >= 0 && id < a.num_valid ? id / a.a_div : 0;
+  int64_t row = direct ? blk / a.a_div : (id >= 0 && id < a.num_valid ? id / a.a_div : 0);
   if (row >= a.ntok) {
     atomicOr(a.err, EMBER_ERR_ROW_INDEX);
     row = 0;
@@ -1085,7 +1100,7 @@ k_moe_gate_up_silu_packed(MoeGuArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  moe_finish<T>(a, acc, tile, w, lane);
+  moe_finish<T>(a, acc, tile, w, lane, id);
 }
 
 // Packs the routed experts' W [E, 2I, H] (strides wes, ws) into k_moe_gate_up_silu_packed's
@@ -1347,6 +1362,46 @@ int ember_moe_gate_up_silu_pack_weight(const void* w, int64_t w_expert_stride, i
     hipLaunchKernelGGL(k_moe_gu_pack<__bf16>, grid, dim3(256), 0, st, static_cast<const __bf16*>(w), w_expert_stride,
                        w_row_stride, static_cast<__bf16*>(packed), static_cast<int>(hidden), static_cast<int>(inter),
                        pieces);
+  return launch_status();
+}
+
+int ember_moe_gate_up_silu_direct(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
+                                  int dtype, int64_t num_experts, int64_t hidden, int64_t inter, const void* topk_ids,
+                                  int id_bytes, int64_t num_assignments, int64_t top_k, int64_t half_slabs, void* out,
+                                  int64_t out_row_stride, void* stream) {
+  if (num_assignments == 0) return EMBER_OK;
+  if (topk_ids == nullptr || (id_bytes != 4 && id_bytes != 8) || (half_slabs != 0 && half_slabs != 1) ||
+      num_assignments < 0 || num_assignments > kMoeMaxBlocks || top_k < 1 || num_assignments % top_k != 0 ||
+      num_assignments / top_k > num_tokens)
+    return EMBER_EINVAL;
+  MoeGuArgs a{};
+  // moe_setup's index checks stand in for the routing ids here (never read as such)
+  const int32_t* ids = static_cast<const int32_t*>(topk_ids);
+  const int rc = moe_setup(a, x, x_row_stride, num_tokens, packed_w, 0, 0, true, dtype, num_experts, hidden, inter,
+                           ids, ids, num_assignments, num_assignments, top_k, 1, nullptr, 0, out, out_row_stride);
+  if (rc != EMBER_OK) return rc;
+  a.sorted_ids = nullptr;
+  a.block_expert = nullptr;
+  a.topk = topk_ids;
+  a.id_bytes = id_bytes;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint32_t slabs = static_cast<uint32_t>(inter / kGuSlab);
+  const uint32_t na = static_cast<uint32_t>(num_assignments);
+  if (half_slabs) {
+    if (dtype == EMBER_F16)
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES, 2>), dim3(2 * slabs, 1u, na),
+                         dim3(2 * kWave), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES, 2>), dim3(2 * slabs, 1u, na),
+                         dim3(2 * kWave), 0, st, a);
+  } else {
+    if (dtype == EMBER_F16)
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<_Float16, EMBER_MOE_PACKED_STAGES, 4>), dim3(slabs, 1u, na),
+                         dim3(kGuWaves * kWave), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_moe_gate_up_silu_packed<__bf16, EMBER_MOE_PACKED_STAGES, 4>), dim3(slabs, 1u, na),
+                         dim3(kGuWaves * kWave), 0, st, a);
+  }
   return launch_status();
 }
 

@@ -236,10 +236,40 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
     return out
 
 
+def moe_gate_up_silu_direct(x: Tensor, topk_ids: Tensor, packed: PackedExperts, *,
+                            half_slabs: bool = False) -> Tensor:
+    """act [N * k, I] straight from the routing ids, without moe_align
+    (`ember_moe_gate_up_silu_direct`): one workgroup per (assignment, slab). Bit-identical to
+    moe_align + moe_gate_up_silu; meant for one token, whose k experts are distinct (an
+    expert picked by several assignments is read once per assignment)."""
+    assert x.dim() == 2 and topk_ids.dim() == 2, (x.shape, topk_ids.shape)
+    _require_device("moe_gate_up_silu_direct", x, topk_ids, packed.packed)
+    n, k = topk_ids.shape
+    if (packed.hidden, packed.dtype, packed.device) != (x.shape[1], x.dtype, x.device) or n > x.shape[0]:
+        raise ValueError("moe_gate_up_silu_direct: the packed weight, x and topk_ids do not match")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"moe_gate_up_silu_direct: int32/int64 ids expected, got {topk_ids.dtype}")
+    ids = topk_ids.contiguous()
+    out = torch.empty((n * k, packed.inter), dtype=x.dtype, device=x.device)
+    if n * k == 0:
+        return out
+    _launch("ember_moe_gate_up_silu_direct", _lib.load().ember_moe_gate_up_silu_direct, x.device,
+            x.data_ptr(), x.stride(0), x.shape[0], packed.packed.data_ptr(), _lib.dtype_tag(x.dtype),
+            packed.num_experts, packed.hidden, packed.inter, ids.data_ptr(), ids.element_size(), n * k, k,
+            int(bool(half_slabs)), out.data_ptr(), out.stride(0))
+    if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_EXPERT_ID:
+        raise IndexError("emberserve_amd.moe_gate_up_silu_direct: expert id out of range")
+    return out
+
+
 def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None,
                       packed: PackedExperts | None = None) -> Tensor:
     """moe_align + moe_gate_up_silu: the routed experts' activations [N * k, I] in
     assignment order (the `act` of moe_triton.py:341)."""
+    if (packed is not None and num_splits is None and topk_ids.shape[0] == 1 and x.is_cuda
+            and fused_enabled(x) and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+        # one token: its k experts are distinct, so no alignment is needed (the same bits)
+        return moe_gate_up_silu_direct(x, topk_ids, packed)
     sorted_ids, block_expert, num_valid = moe_align(topk_ids, w_gate_up.shape[0])
     return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1],
                             num_splits=num_splits, packed=packed)

@@ -16,7 +16,8 @@ if not torch.cuda.is_available():
     pytest.skip("needs a GPU", allow_module_level=True)
 
 from emberserve_amd import _lib  # noqa: E402
-from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu, pack_moe_gate_up_weight  # noqa: E402
+from emberserve_amd.moe import (fused_moe_gate_up, moe_align, moe_gate_up_silu, moe_gate_up_silu_direct,  # noqa: E402
+                                pack_moe_gate_up_weight)
 from oracle import ref_ops as ref  # noqa: E402
 from tests.helpers import check_gate_up  # noqa: E402
 
@@ -154,3 +155,32 @@ def test_moe_packed_half_slabs_equal_full_slabs(n):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     with pytest.raises(ValueError):
         moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=2, packed=packed, half_slabs=True)
+
+
+# ---- straight from the routing ids (ember_moe_gate_up_silu_direct) ----
+@pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
+@pytest.mark.parametrize("n", [1, 3])
+@pytest.mark.parametrize("half", [False, True])
+def test_moe_direct_equals_the_aligned_path(id_dtype, n, half):
+    """Each assignment alone in lane 0 of its workgroup: the same products in the same order
+    as in its aligned block, so bit-identical (3 tokens: experts picked twice are read twice,
+    still the same bits)."""
+    x, w, ids = _inputs(n, torch.bfloat16, seed=400 + n)
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    packed = pack_moe_gate_up_weight(dw)
+    sorted_ids, block_expert, nv = moe_align(dids, E)
+    want = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=1, packed=packed, half_slabs=False)
+    got = moe_gate_up_silu_direct(dx, dids.to(id_dtype), packed, half_slabs=half)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    if n == 1:  # fused_moe_gate_up takes this path for one token
+        assert torch.equal(fused_moe_gate_up(dx, dids, dw, packed=packed).view(torch.int16), want.view(torch.int16))
+
+
+def test_moe_direct_bad_expert_sets_error_bit():
+    x, w, ids = _inputs(1, torch.bfloat16, seed=5)
+    dw = w.to(DEV)
+    bad = ids.clone()
+    bad[0, 2] = E + 3
+    moe_gate_up_silu_direct(x.to(DEV), bad.to(DEV), pack_moe_gate_up_weight(dw))
+    torch.cuda.synchronize()
+    assert _lib.read_errors(clear=True) & _lib.ERR_EXPERT_ID
