@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -82,7 +82,8 @@ SIGNATURES: dict[str, list] = {
     "ember_moe_gate_up_silu_packed": [_p, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64,
                                       _p, _i64, _p, _i64, _p],
     "ember_moe_align_padded_size": [_i64, _i64, _i64],
-    "ember_moe_align": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
+    "ember_moe_align_workspace_bytes": [_i64, _i64],
+    "ember_moe_align": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
     "ember_read_errors": [ctypes.POINTER(ctypes.c_uint32), _i32],
     "ember_abi_version": [],
     "ember_status_string": [_i32],
@@ -93,6 +94,7 @@ _RESTYPE = {"ember_status_string": ctypes.c_char_p, "ember_paged_decode_workspac
             "ember_gate_up_silu_workspace_bytes": ctypes.c_int64,
             "ember_moe_gate_up_silu_workspace_bytes": ctypes.c_int64,
             "ember_moe_align_padded_size": ctypes.c_int64,
+            "ember_moe_align_workspace_bytes": ctypes.c_int64,
             "ember_paged_decode_noalloc_max_bytes": ctypes.c_int64}
 
 

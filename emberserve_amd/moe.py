@@ -50,9 +50,12 @@ def moe_align_torch(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) 
     return sorted_ids, block_expert, num_valid
 
 
-def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tuple[Tensor, Tensor, int]:
+def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M, *,
+              grid: bool = True) -> tuple[Tensor, Tensor, int]:
     """The block-aligned expert layout of moe_triton.py:215-254 (the single-launch form of
-    :97-160): one launch of `ember_moe_align` on the GPU, no host sync, no workspace.
+    :97-160): `ember_moe_align` on the GPU, no host sync. Past 3072 assignments it runs as a
+    count launch and a placement launch over up to 64 workgroups with a small count-table
+    workspace (grid=False keeps the one-workgroup form, the same layout).
     Returns (sorted_ids [max_padded] int32, block_expert [max_blocks] int32, num_valid):
     assignments id = token * k + choice grouped by expert in ascending id order, each
     expert's run padded to a multiple of block_m with num_valid, and the expert of every
@@ -71,8 +74,11 @@ def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = BLOCK_M) -> tup
                          f"block_m {block_m})")
     sorted_ids = torch.empty((max_padded,), dtype=torch.int32, device=flat.device)
     block_expert = torch.empty((max_padded // block_m,), dtype=torch.int32, device=flat.device)
+    ws_bytes = lib.ember_moe_align_workspace_bytes(num_valid, num_experts) if grid else 0
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=flat.device) if ws_bytes > 0 else None
     _launch("ember_moe_align", lib.ember_moe_align, flat.device, flat.data_ptr(), flat.element_size(), num_valid,
-            num_experts, block_m, sorted_ids.data_ptr(), max_padded, block_expert.data_ptr(), max_padded // block_m)
+            num_experts, block_m, sorted_ids.data_ptr(), max_padded, block_expert.data_ptr(), max_padded // block_m,
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws_bytes)
     if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_EXPERT_ID:
         raise IndexError(f"emberserve_amd.moe_align: expert id outside [0, {num_experts})")
     return sorted_ids, block_expert, num_valid

@@ -491,21 +491,30 @@ int64_t ember_moe_gate_up_silu_workspace_bytes(int64_t num_valid, int64_t inter,
  * block_m), -1 for invalid arguments (the max_padded of moe_triton.py:249). */
 int64_t ember_moe_align_padded_size(int64_t num_valid, int64_t num_experts, int64_t block_m);
 
-/* The routed experts' block-aligned layout in one launch (one workgroup), replacing
- * moe_align of emberserve/model/moe_triton.py:215-254 (its single-launch form is
- * _moe_align_kernel, :97-160). topk_ids: num_valid = tokens * top_k expert ids (id_bytes 4
- * or 8, contiguous, assignment id = position). Writes
+/* Bytes of workspace for the grid form of ember_moe_align at num_valid assignments (0 when
+ * the one-workgroup form is used at that size), -1 for invalid arguments: an int32 count
+ * table [segments][num_experts] over at most 64 segments of the assignments. */
+int64_t ember_moe_align_workspace_bytes(int64_t num_valid, int64_t num_experts);
+
+/* The routed experts' block-aligned layout, replacing moe_align of
+ * emberserve/model/moe_triton.py:215-254 (its single-launch form is _moe_align_kernel,
+ * :97-160). topk_ids: num_valid = tokens * top_k expert ids (id_bytes 4 or 8, contiguous,
+ * assignment id = position). Writes
  *   sorted_ids [max_padded]: each expert's assignment ids in ascending order, its run padded
  *     with num_valid to a multiple of block_m, experts in ascending order, num_valid after
  *     the last run;
  *   block_expert [max_blocks = max_padded / block_m]: the expert of each block, num_experts
  *     past the last used block.
  * max_padded must equal ember_moe_align_padded_size(...). 1 <= num_experts <= 1024. An id
- * outside [0, num_experts) is left out of the layout and sets EMBER_ERR_EXPERT_ID. No host
- * synchronisation, no workspace, no memset: safe to capture in a HIP graph. */
+ * outside [0, num_experts) is left out of the layout and sets EMBER_ERR_EXPERT_ID.
+ * workspace (may be null) holds the grid form's count table: with at least
+ * ember_moe_align_workspace_bytes(...) bytes, a count launch over up to 64 workgroups and a
+ * placement launch over the same segments; otherwise (and always at num_valid <= 3072) one
+ * workgroup in one launch. Both give the same layout. The workspace needs no clearing; no
+ * host synchronisation, no memset: safe to capture in a HIP graph. */
 int ember_moe_align(const void* topk_ids, int id_bytes, int64_t num_valid, int64_t num_experts, int64_t block_m,
                     int32_t* sorted_ids, int64_t max_padded, int32_t* block_expert, int64_t max_blocks,
-                    void* stream);
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -358,6 +358,27 @@ def test_gate_up_silu_workspace_plan():
     assert lib.ember_gate_up_silu_workspace_bytes(16, 4096, 128, 0) == -1
 
 
+def test_moe_align_workspace_and_abi_validation():
+    """The grid form's count table: [segments][E] int32 over ceil(num_valid / 2048) segments,
+    at most 64, used past 3072 assignments (0 bytes below); argument checks before any launch."""
+    lib = _lib.load()
+    assert lib.ember_moe_align_workspace_bytes(3072, 64) == 0
+    assert lib.ember_moe_align_workspace_bytes(3073, 64) == 2 * 64 * 4
+    assert lib.ember_moe_align_workspace_bytes(8193, 64) == 5 * 64 * 4
+    assert lib.ember_moe_align_workspace_bytes(49152, 64) == 24 * 64 * 4
+    assert lib.ember_moe_align_workspace_bytes(10 ** 7, 256) == 64 * 256 * 4
+    assert lib.ember_moe_align_workspace_bytes(-1, 64) == -1
+    assert lib.ember_moe_align_workspace_bytes(100, 1025) == -1
+    mp = lib.ember_moe_align_padded_size(100, 8, 16)
+
+    def call(nv=100, e=8, bm=16, padded=mp, blocks=mp // 16, ws=None, ws_bytes=0, id_bytes=8):
+        return lib.ember_moe_align(None, id_bytes, nv, e, bm, None, padded, None, blocks, ws, ws_bytes, None)
+    for bad in (dict(id_bytes=2), dict(e=0), dict(e=1025), dict(bm=0), dict(padded=mp + 16), dict(blocks=1),
+                dict(ws_bytes=-1), dict(ws_bytes=64)):
+        assert call(**bad) == 1, bad
+    assert call() == 1  # null pointers
+
+
 def test_gate_up_silu_abi_validation():
     lib = _lib.load()
 

@@ -106,3 +106,44 @@ def test_align_in_a_graph_replays_fresh_ids():
         torch.cuda.synchronize()
         want_s, want_b, _ = ref.moe_align(new, e, 16)
         assert s.cpu().tolist() == want_s and b.cpu().tolist() == want_b, rep
+
+
+@pytest.mark.parametrize("n,e,k", [(512, 64, 6), (513, 64, 6), (1366, 64, 6), (8192, 64, 6), (4096, 256, 8),
+                                   (20000, 1024, 3), (70000, 64, 6)])
+def test_grid_form_matches_one_workgroup_form(n, e, k):
+    """Past 3072 assignments the layout comes from a count launch and a placement launch
+    over up to 64 workgroups; it equals the one-workgroup form slot for slot and the oracle
+    (512 x 6 is the last one-workgroup size at k = 6, 513 x 6 the first grid size; 70000 x 6
+    spreads 420000 assignments over the 64-workgroup cap, past the register-held spans)."""
+    g = torch.Generator().manual_seed(n * 7 + e)
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(n)])
+    lib = _lib.load()
+    print(f"moe_align grid ids {(n, k)} E={e} workspace {lib.ember_moe_align_workspace_bytes(n * k, e)} B",
+          flush=True)
+    s1, b1, _ = moe_align(ids.to(DEV), e, grid=True)
+    s0, b0, _ = moe_align(ids.to(DEV), e, grid=False)
+    assert torch.equal(s1, s0) and torch.equal(b1, b0)
+    if n * k <= 50000:
+        want_s, want_b, _ = ref.moe_align(ids, e, 16)
+        assert s1.cpu().tolist() == want_s and b1.cpu().tolist() == want_b
+
+
+def test_grid_form_skewed_and_bad_ids(monkeypatch):
+    """All assignments on a few experts (long runs crossing segment boundaries) and an out-of-range
+    id in the grid form: flagged, left out, the rest as the one-workgroup form places them."""
+    g = torch.Generator().manual_seed(11)
+    skew = (torch.rand(3000, 4, generator=g) ** 6 * 12).long()
+    s1, b1, _ = moe_align(skew.to(DEV), 12, 16)
+    want_s, want_b, _ = ref.moe_align(skew, 12, 16)
+    assert s1.cpu().tolist() == want_s and b1.cpu().tolist() == want_b
+    bad = skew.clone()
+    bad[1234, 2] = 40
+    monkeypatch.setenv("EMBERSERVE_CHECK_INDICES", "1")
+    with pytest.raises(IndexError, match="expert id"):
+        moe_align(bad.to(DEV), 12, 16)
+    monkeypatch.delenv("EMBERSERVE_CHECK_INDICES")
+    s1, b1, _ = moe_align(bad.to(DEV), 12, 16)
+    s0, b0, _ = moe_align(bad.to(DEV), 12, 16, grid=False)
+    _lib.read_errors(clear=True)
+    assert torch.equal(s1, s0) and torch.equal(b1, b0)
+    assert (s1 == 1234 * 4 + 2).sum().item() == 0  # assignment 4938 is left out
