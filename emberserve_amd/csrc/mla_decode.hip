@@ -86,6 +86,12 @@ constexpr bool kMlaPairSync = EMBER_MLA_PAIR_SYNC != 0;  // pair-local exchange 
 #define EMBER_MLA_STAGED 1
 #endif
 constexpr bool kMlaStaged = EMBER_MLA_STAGED != 0;  // small grids: rows staged through LDS
+#ifndef EMBER_MLA_MERGE_APART
+#define EMBER_MLA_MERGE_APART 4
+#endif
+// Split counts from which the MFMA kernels leave the split-K merge to k_mla_merge (a second
+// launch spread over many workgroups) instead of the last split to arrive.
+constexpr int kMlaMergeApart = EMBER_MLA_MERGE_APART;
 constexpr int kMlaDL = 512;
 constexpr int kMlaDR = 64;
 
@@ -113,6 +119,7 @@ struct MlaArgs {
   float* part_l;
   float* part_o;               // [splits][nseq][nh][dl]
   uint32_t* counters;          // [nseq][nh] split arrivals (MFMA kernel), zero between launches
+  int32_t merge_apart;         // MFMA kernels: publish the partials only, k_mla_merge merges
   uint32_t* err;
 };
 
@@ -275,6 +282,7 @@ __device__ __forceinline__ void mla_finish(const MlaArgs& a, unsigned char* lds,
     for (int j = 0; j < NJ; ++j)
       store_coherent<4>(rs, (hh * DL + p4 + 4 * PARTS * j) * int(sizeof(float)), acc[j]);
   }
+  if (a.merge_apart) return;
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __shared__ int is_last;
   __syncthreads();
@@ -985,6 +993,62 @@ k_mla_reduce(MlaArgs a) {
   }
 }
 
+// The split-K merge of the MFMA kernels as its own launch: one thread per 4 contiguous d of
+// a (sequence, head) row, all of whose splits' partials it merges online, eight splits'
+// loads in flight at a time. One 64-lane workgroup per 256 output floats spreads a lone
+// sequence's partials (16 heads x 512 floats per split) over 32 CUs.
+template <typename TO, int DL>
+__global__ void __launch_bounds__(kWave)
+k_mla_merge(MlaArgs a) {
+  constexpr int TPR = DL / 4;
+  constexpr int kChunk = 8;
+  const int t = blockIdx.x * kWave + threadIdx.x;
+  const int row = t / TPR;  // sequence * nh + head
+  if (row >= a.nseq * a.nh) return;
+  const int d = (t % TPR) * 4;
+  const int64_t stride = int64_t(a.nseq) * a.nh;
+  float gm = -INFINITY, gl = 0.f;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < a.splits; c0 += kChunk) {
+    float ms[kChunk], ls[kChunk];
+    f32x4 v[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      ms[u] = -INFINITY;
+      ls[u] = 0.f;
+      v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (c0 + u < a.splits) {
+        const int64_t r = (c0 + u) * stride + row;
+        ms[u] = a.part_m[r];
+        ls[u] = a.part_l[r];
+        // part_o starts 8 bytes past a 16-byte boundary when splits x rows is odd
+        const float2 lo = *reinterpret_cast<const float2*>(a.part_o + r * DL + d);
+        const float2 hi = *reinterpret_cast<const float2*>(a.part_o + r * DL + d + 2);
+        v[u] = f32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+    }
+    float cm = gm;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) cm = fmaxf(cm, ms[u]);
+    const float alpha = gm == -INFINITY ? 0.f : exp2_fast(gm - cm);
+    gl *= alpha;
+    acc *= alpha;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const float wt = ms[u] == -INFINITY ? 0.f : exp2_fast(ms[u] - cm);
+      gl += wt * ls[u];
+      acc += wt * v[u];
+    }
+    gm = cm;
+  }
+  const int b = row / a.nh;
+  const int h = row - b * a.nh;
+  Pack<TO, 4> r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r.v[e] = from_f32<TO>(acc[e] / gl);
+  store_pack<TO, 4>(static_cast<TO*>(a.out) + b * a.o_sb + h * a.o_sh + d, r);
+}
+
 template <typename TQ>
 int launch_any_q(int cdt, const MlaArgs& a, dim3 grid, hipStream_t st) {
   switch (cdt) {
@@ -1099,6 +1163,7 @@ int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_str
     // streams per workgroup: half the serial tiles per stream, one workgroup per CU.
     const int ncu = device_cu_count();
     const bool small = ncu > 0 && progs * num_splits * 2 <= ncu;
+    a.merge_apart = num_splits >= kMlaMergeApart ? 1 : 0;
     if (q_dtype == EMBER_F16) {
       if (small && kMlaStaged)
         k_mla_lds<_Float16, kMlaDL, kMlaDR><<<grid, 4 * kWave, 0, st>>>(a);
@@ -1113,6 +1178,14 @@ int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_str
         k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairsSmall, kMlaPairSync><<<grid, kMlaPairsSmall * 2 * kWave, 0, st>>>(a);
       else
         k_mla_mfma<__bf16, kMlaDL, kMlaDR, kMlaPairs, kMlaPairSync><<<grid, kMlaPairs * 2 * kWave, 0, st>>>(a);
+    }
+    if (a.merge_apart) {
+      const int64_t threads = num_seqs * num_heads * (kMlaDL / 4);
+      const uint32_t blocks = static_cast<uint32_t>((threads + kWave - 1) / kWave);
+      if (q_dtype == EMBER_F16)
+        k_mla_merge<_Float16, kMlaDL><<<blocks, kWave, 0, st>>>(a);
+      else
+        k_mla_merge<__bf16, kMlaDL><<<blocks, kWave, 0, st>>>(a);
     }
   } else {
     dim3 grid(static_cast<uint32_t>(num_seqs * num_heads), static_cast<uint32_t>(num_splits));

@@ -33,7 +33,7 @@ from .paged_decode import num_sms
 
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 BLOCK_MULTIPLE = 16
-MAX_SPLITS = 64
+MAX_SPLITS = 128
 TILE = 32                 # keys per kernel tile
 MAX_DIM = 1024            # DL + DR of the fp32 kernel
 
@@ -44,12 +44,13 @@ def mla_num_splits(batch: int, device: torch.device, *, num_heads: int = 16,
 
     `EMBERSERVE_TRITON_SPLITS=<n>` forces a value. Otherwise the grid is sized to one
     (sequence, 16-head chunk, split) workgroup per compute unit, and with `max_context`
-    (the table width in keys) to about sqrt(max_context / 16) splits: a split's fixed cost
-    (three dependent reads before its first tile, the merge after its last) wants more
-    keys per split as contexts grow. Measured on MI355X (bf16, 16 heads, block 16), best
-    split counts: B = 1 at 320 / 1024 / 4096 / 32768 keys: 4 / 8 / 16 / 48 (16.5, 19.7,
-    29.4, 63.7 us); B = 128 x 2048: 2 (65.6 us, 4.6 TB/s); B = 256 x 2048: 1 (5.4 TB/s).
-    The reference's signature (batch, device) stays valid."""
+    (the table width in keys) to about sqrt(max_context / 4) splits, at least 16 keys
+    each: a split's fixed cost (three dependent reads before its first tile, its share of
+    the merge) wants more keys per split as contexts grow. From 4 splits the merge is its
+    own wide launch, which makes splits cheap. Measured on MI355X (bf16, 16 heads, block
+    16), best split counts: B = 1 at 320 / 1024 / 4096 / 8192 / 32768 keys: 6-8 / 16 / 32
+    / 48-64 / 128 (10.2, 11.3, 15.1, 18.6, 32.7 us); B = 128 x 2048: 2 (4.6 TB/s); B = 256
+    x 2048: 1 (5.4 TB/s). The reference's signature (batch, device) stays valid."""
     forced = os.environ.get("EMBERSERVE_TRITON_SPLITS")
     if forced:
         return max(1, int(forced))
@@ -57,7 +58,8 @@ def mla_num_splits(batch: int, device: torch.device, *, num_heads: int = 16,
     programs = max(1, batch * chunks)
     want = max(1, num_sms(device) // programs)
     if max_context is not None:
-        want = min(want, max(1, math.isqrt(max(0, max_context) // 16)))
+        keys = max(0, max_context)
+        want = min(want, max(1, math.isqrt(keys // 4)), max(1, -(-keys // 16)))
     return max(1, min(MAX_SPLITS, want))
 
 

@@ -348,7 +348,8 @@ int64_t ember_mla_decode_workspace_bytes(int64_t num_seqs, int64_t num_heads, in
  * fp16/bf16 q and cache of one dtype at kv_lora_rank 512, rope_dim 64 (DeepSeek-V2/V3,
  * Moonlight) with 16-byte aligned operands run on MFMA with the reference kernel's tl.dot
  * numerics (fp32 scores, probabilities rounded to the cache dtype for P.V); every other case
- * computes in fp32. */
+ * computes in fp32. The MFMA path merges 2-3 splits in the last split to arrive and 4 or more
+ * in a second launch spread over many workgroups. */
 int ember_mla_decode(const void* q_c, int64_t qc_seq_stride, int64_t qc_head_stride,
                      const void* q_pe, int64_t qpe_seq_stride, int64_t qpe_head_stride, int q_dtype,
                      const void* latent_cache, int64_t num_blocks, int64_t block_size,

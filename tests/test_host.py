@@ -289,9 +289,10 @@ def test_mla_decode_abi_and_split_rule(monkeypatch):
     dev = torch.device("cpu")
     assert md.mla_num_splits(128, dev) == 2                          # 128 workgroups -> 256
     assert md.mla_num_splits(1, dev) == md.MAX_SPLITS
-    assert md.mla_num_splits(1, dev, max_context=320) == 4           # ~sqrt(context / 16)
-    assert md.mla_num_splits(1, dev, max_context=4096) == 16
-    assert md.mla_num_splits(1, dev, max_context=32768) == 45
+    assert md.mla_num_splits(1, dev, max_context=320) == 8           # ~sqrt(context / 4)
+    assert md.mla_num_splits(1, dev, max_context=4096) == 32
+    assert md.mla_num_splits(1, dev, max_context=32768) == 90
+    assert md.mla_num_splits(1, dev, max_context=48) == 3            # at least 16 keys a split
     assert md.mla_num_splits(1, dev, max_context=16) == 1
     assert md.mla_num_splits(8, dev, num_heads=128, max_context=4096) == 4   # 64 workgroups -> 256
     assert md.mla_num_splits(128, dev, max_context=320) == 2

@@ -165,10 +165,12 @@ def test_fp32_cache_and_unaligned_strides_take_the_fp32_kernel(dtype):
 @pytest.mark.parametrize("heads", [1, 20, 128])
 def test_head_counts(heads):
     """One head (15 padded MFMA columns), 20 heads (a full and a partial 16-head chunk) and
-    DeepSeek-V3's 128 heads (8 chunks re-reading each row)."""
+    DeepSeek-V3's 128 heads (8 chunks re-reading each row), at one split, the default and
+    5 (merged by its own launch; with one head, 15 partial rows put the partial block 8
+    bytes past a 16-byte boundary)."""
     ctx_lens = [77, 513, 1]
     q, lat, bt, ctx = gen.mla_decode_inputs(ctx_lens, heads, DL, DR, 16, torch.bfloat16, seed=4)
-    for splits in (1, None):
+    for splits in (1, None, 5):
         _say(f"mla decode heads {heads} splits {splits}")
         got = mla_decode(q.to(DEV), lat.to(DEV), bt.to(DEV), ctx.to(DEV), SCALE, DL, num_splits=splits)
         torch.cuda.synchronize()
@@ -232,10 +234,10 @@ def test_split_rule_shapes_only(monkeypatch):
     cus = num_sms(dev)
     assert mla_num_splits(128, dev) == max(1, cus // 128)
     assert mla_num_splits(1, dev, max_context=16) == 1
-    assert mla_num_splits(1, dev, max_context=320) == min(4, cus)  # ~sqrt(context / 16)
-    assert mla_num_splits(1, dev, max_context=4096) == min(16, cus)
-    assert mla_num_splits(1, dev, max_context=1 << 20) == min(64, cus)
-    assert mla_num_splits(4, dev, num_heads=128, max_context=1 << 20) == max(1, min(64, cus // 32))
+    assert mla_num_splits(1, dev, max_context=320) == min(8, cus)  # ~sqrt(context / 4)
+    assert mla_num_splits(1, dev, max_context=4096) == min(32, cus)
+    assert mla_num_splits(1, dev, max_context=1 << 20) == min(128, cus)
+    assert mla_num_splits(4, dev, num_heads=128, max_context=1 << 20) == max(1, min(128, cus // 32))
 
 
 def test_graph_replay_with_changing_contexts():
