@@ -443,6 +443,27 @@ def _ops(torch, ops, tables):
         out.append(Op("moe_align+gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts, align each call",
                       nbytes, make, lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes))
 
+    def moe_prefill(cfg, n):
+        """The routed experts' gate_up + silu_and_mul at prefill batches (Moonlight geometry):
+        what fused_moe_gate_up runs from 3072 assignments (moe_align over 256-row blocks + the
+        MFMA GEMM with the activation in its epilogue) beside the 16-block kernel of the
+        reference's structure (moe_triton.py:332-340: 16-row blocks of one expert). Alignment
+        is launched in both. MFMA-bound: 2·N·k·2I·H flops; bytes as in the decode rows."""
+        from emberserve_amd.moe import moe_align, moe_gate_up_silu, moe_gate_up_silu_gemm
+        h, inter, ne, k = 2048, 1408, 64, 6
+        seed(350 + n)
+        ids = torch.stack([torch.randperm(ne, generator=gi).to(dev)[:k] for _ in range(n)])
+
+        def make(i):
+            return randn((n, h), bf, 360 + i, std=0.5), randn((ne, 2 * inter, h), bf, 365 + i, std=h ** -0.5)
+        wbytes = ne * 2 * inter * h * 2
+        nbytes = wbytes + n * h * 2 + n * k * inter * 2
+        shape = f"moonlight: N={n} top-{k} of {ne} experts, w[{ne},{2 * inter},{h}] bf16"
+        out.append(Op("moe_gate_up_silu_gemm", cfg, shape + " (align 256 + MFMA GEMM, 128-column tiles)", nbytes,
+                      make, lambda a: moe_gate_up_silu_gemm(a[0], a[1], ids, column_tile=128), wbytes))
+        out.append(Op("moe_align+gate_up_silu", cfg, shape + " (align 16 + 16-block kernel)", nbytes, make,
+                      lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes))
+
     def moe_align_row(cfg, n, ne=64, k=6):
         """ember_moe_align alone (moe_triton.py:215-254's layout in one launch): bytes are the
         ids read plus the layout written."""
@@ -504,6 +525,8 @@ def _ops(torch, ops, tables):
         gate_up_prefill("mlp_prefill", t, 3584, 18944, "qwen2.5-7b")
     for n in (1, 8, 64):
         moe_gate_up("moe", n)
+    for n in (1024, 8192):
+        moe_prefill("moe_prefill", n)
     for n in (1, 64, 8192):
         moe_align_row("moe", n)
 

@@ -106,9 +106,17 @@ struct GemmArgs {
   void* out;
   int64_t os;
   int T, H, I;
+  // routed experts (MOE kernels only): token tiles are kGemmBM-assignment blocks of the
+  // block-aligned layout; block b's rows are assignments sorted_ids[b kGemmBM + r] (padding:
+  // >= num_valid) of expert block_expert[b], x row = assignment / top_k, output row = the
+  // assignment; wes = elements between experts' [2I, H] weights
+  const int32_t* sorted_ids;
+  const int32_t* block_expert;
+  int num_valid, top_k, E, ntok;
+  int64_t wes;
 };
 
-template <typename T, int BNG>
+template <typename T, int BNG, bool MOE>
 __global__ void __launch_bounds__(512, 1)
 k_gate_up_silu_gemm(GemmArgs a) {
   using M = GemmMfma<T>;
@@ -152,6 +160,11 @@ k_gate_up_silu_gemm(GemmArgs a) {
 
   const T* X = static_cast<const T*>(a.x);
   const T* W = static_cast<const T*>(a.w);
+  if (MOE) {
+    const int e = a.block_expert[mt];  // uniform
+    if (e < 0 || e >= a.E) return;     // past the layout's used blocks
+    W += static_cast<int64_t>(e) * a.wes;
+  }
   // This wave's load instructions of a double stage: instruction ins moves rows
   // 8 (ins % 32) + lane / 8 of region ins / 32-ish (weight rows first, then x rows); lane l
   // loads 16-byte chunk (l % 8) ^ (row % 8) of its row into slot l of the 1 KiB block.
@@ -167,7 +180,14 @@ k_gate_up_silu_gemm(GemmArgs a) {
       src[i] = W + static_cast<int64_t>(wr) * a.ws + 8 * c;
     } else {
       const int xr = row - 2 * BNG;
-      src[i] = X + static_cast<int64_t>(min(m0 + xr, a.T - 1)) * a.xs + 8 * c;  // padded tokens: the last real one
+      int64_t xrow;
+      if (MOE) {  // padding assignments read token 0 and store nothing
+        const int id = a.sorted_ids[m0 + xr];
+        xrow = id >= 0 && id < a.num_valid ? min(id / a.top_k, a.ntok - 1) : 0;
+      } else {
+        xrow = min(m0 + xr, a.T - 1);  // padded tokens: the last real one
+      }
+      src[i] = X + xrow * a.xs + 8 * c;
     }
     dst[i] = ins * 1024;  // the weight region is rows 0 .. 2 BNG - 1, the x region follows
   }
@@ -234,8 +254,13 @@ k_gate_up_silu_gemm(GemmArgs a) {
   T* out = static_cast<T*>(a.out);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int tok = m0 + 64 * q + 16 * u + n;
-    if (tok < a.T) {
+    int tok = m0 + 64 * q + 16 * u + n;
+    bool real = tok < a.T;
+    if (MOE) {  // the assignment's own output row
+      tok = a.sorted_ids[tok];
+      real = tok >= 0 && tok < a.num_valid;
+    }
+    if (real) {
 #pragma unroll
       for (int t = 0; t < NT / 2; ++t) {
         const int col = n0 + (BNG / 2) * grp + 16 * t + 4 * g;
@@ -253,11 +278,11 @@ k_gate_up_silu_gemm(GemmArgs a) {
   }
 }
 
-template <typename T, int BNG>
+template <typename T, int BNG, bool MOE = false>
 int launch_gemm(const GemmArgs& a, hipStream_t st) {
   const int64_t grid = cdiv(a.T, kGemmBM) * (a.I / BNG);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
+  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, MOE>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
   return launch_status();
 }
 
@@ -280,9 +305,40 @@ extern "C" int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, cons
       w_row_stride % 8 != 0 || out_row_stride % 4 != 0)
     return EMBER_EINVAL;
   GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(tokens),
-             static_cast<int>(hidden), static_cast<int>(inter)};
+             static_cast<int>(hidden), static_cast<int>(inter), nullptr, nullptr, 0, 1, 0, 0, 0};
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16)
     return column_tile == 64 ? launch_gemm<_Float16, 64>(a, st) : launch_gemm<_Float16, 128>(a, st);
   return column_tile == 64 ? launch_gemm<__bf16, 64>(a, st) : launch_gemm<__bf16, 128>(a, st);
+}
+
+extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+                                           int64_t w_expert_stride, int64_t w_row_stride, int dtype,
+                                           int64_t num_experts, int64_t hidden, int64_t inter,
+                                           const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
+                                           int64_t num_valid, int64_t top_k, int64_t column_tile, void* out,
+                                           int64_t out_row_stride, void* stream) {
+  using namespace ember;
+  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  if (num_blocks < 0 || num_valid < 0 || num_tokens < 1 || top_k < 1 || num_experts < 1 || num_blocks > (1 << 22) ||
+      num_valid > INT32_MAX / 2 || num_tokens > INT32_MAX || hidden < 64 || hidden % 64 != 0 ||
+      hidden > (int64_t(1) << 20) || (column_tile != 64 && column_tile != 128) || inter < column_tile ||
+      inter % column_tile != 0 || inter > (int64_t(1) << 28))
+    return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || w == nullptr || out == nullptr || sorted_ids == nullptr || block_expert == nullptr ||
+      !aligned16(x) || !aligned16(w) || !aligned16(out))
+    return EMBER_EINVAL;
+  if (x_row_stride < hidden || w_row_stride < hidden || w_expert_stride < 2 * inter * w_row_stride ||
+      out_row_stride < inter || x_row_stride % 8 != 0 || w_row_stride % 8 != 0 || w_expert_stride % 8 != 0 ||
+      out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(num_blocks * kGemmBM),
+             static_cast<int>(hidden), static_cast<int>(inter), sorted_ids, block_expert,
+             static_cast<int>(num_valid), static_cast<int>(top_k), static_cast<int>(num_experts),
+             static_cast<int>(num_tokens), w_expert_stride};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16)
+    return column_tile == 64 ? launch_gemm<_Float16, 64, true>(a, st) : launch_gemm<_Float16, 128, true>(a, st);
+  return column_tile == 64 ? launch_gemm<__bf16, 64, true>(a, st) : launch_gemm<__bf16, 128, true>(a, st);
 }

@@ -242,6 +242,48 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
     return out
 
 
+GEMM_BLOCK_M = 256  # rows per block of the prefill GEMM's layout (its token tile)
+# fused_moe_gate_up: the GEMM from this many assignments, the packed 16-block kernel up to
+# PACKED_MAX_ASSIGNMENTS. Measured at Moonlight's geometry (bf16, µs, alignment included;
+# row kernel at its default splits | GEMM at 128-column tiles): 384 assignments 147 | 207,
+# 1536: 223 | 255, 3072: 292 | 272, 6144: 494 | 272, 12288: 823 | 330, 49152: 2727 | 673.
+# The packed kernel: 384 assignments 115 against the row kernel's 136; 1536: 228 against 205.
+GEMM_FROM = 3072
+PACKED_MAX_ASSIGNMENTS = 768
+
+
+def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, column_tile: int = 128) -> Tensor:
+    """act [N * k, I] at prefill sizes (`ember_moe_gate_up_silu_gemm`): moe_align with
+    256-row blocks, then the MFMA GEMM of `gate_up_silu_gemm` over each block's gathered x
+    rows and its expert's weight, silu_and_mul in the epilogue, rows scattered back to
+    assignment order. The first grouped GEMM + silu_and_mul of moe_triton.py:339-340;
+    bit-identical to `moe_gate_up_silu` for every assignment."""
+    assert x.dim() == 2 and w_gate_up.dim() == 3 and topk_ids.dim() == 2, (x.shape, w_gate_up.shape, topk_ids.shape)
+    _require_device("moe_gate_up_silu_gemm", x, w_gate_up, topk_ids)
+    E, two_i, H = w_gate_up.shape
+    inter = two_i // 2
+    n, k = topk_ids.shape
+    if x.shape[1] != H or two_i % 2 or n > x.shape[0]:
+        raise ValueError(f"moe_gate_up_silu_gemm: x {tuple(x.shape)}, w_gate_up {tuple(w_gate_up.shape)} and "
+                         f"topk_ids {tuple(topk_ids.shape)} do not match")
+    sorted_ids, block_expert, num_valid = moe_align(topk_ids, E, GEMM_BLOCK_M)
+    out = torch.empty((num_valid, inter), dtype=x.dtype, device=x.device)
+    if num_valid == 0:
+        return out
+    fits = (x.dtype == w_gate_up.dtype and x.dtype in SUPPORTED_DTYPES and H % 64 == 0
+            and inter % column_tile == 0 and x.stride(1) == 1 and w_gate_up.stride(2) == 1
+            and x.stride(0) % 8 == 0 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and w_gate_up.data_ptr() % 16 == 0)
+    if not fits:
+        raise ValueError(f"moe_gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {inter}, "
+                         f"column_tile {column_tile}, {x.dtype})")
+    _launch("ember_moe_gate_up_silu_gemm", _lib.load().ember_moe_gate_up_silu_gemm, x.device,
+            x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
+            _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
+            block_expert.numel(), num_valid, k, column_tile, out.data_ptr(), out.stride(0))
+    return out
+
+
 def moe_gate_up_silu_direct(x: Tensor, topk_ids: Tensor, packed: PackedExperts, *,
                             half_slabs: bool = False) -> Tensor:
     """act [N * k, I] straight from the routing ids, without moe_align
@@ -270,12 +312,25 @@ def moe_gate_up_silu_direct(x: Tensor, topk_ids: Tensor, packed: PackedExperts, 
 
 def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None,
                       packed: PackedExperts | None = None) -> Tensor:
-    """moe_align + moe_gate_up_silu: the routed experts' activations [N * k, I] in
-    assignment order (the `act` of moe_triton.py:341)."""
-    if (packed is not None and num_splits is None and topk_ids.shape[0] == 1 and x.is_cuda
-            and fused_enabled(x) and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+    """The routed experts' activations [N * k, I] in assignment order (the `act` of
+    moe_triton.py:340): one token over a packed weight straight from the routing ids; from
+    GEMM_FROM assignments the prefill GEMM (`moe_gate_up_silu_gemm`); otherwise moe_align +
+    the 16-block kernel (`moe_gate_up_silu`, packed up to PACKED_MAX_ASSIGNMENTS). Every
+    path gives the same bits as the 16-block kernel at one k split."""
+    aligned = x.is_cuda and fused_enabled(x) and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+    n, k = topk_ids.shape
+    if packed is not None and num_splits is None and n == 1 and aligned:
         # one token: its k experts are distinct, so no alignment is needed (the same bits)
         return moe_gate_up_silu_direct(x, topk_ids, packed)
-    sorted_ids, block_expert, num_valid = moe_align(topk_ids, w_gate_up.shape[0])
-    return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, topk_ids.shape[1],
+    E, two_i, H = w_gate_up.shape
+    if (num_splits is None and n * k >= GEMM_FROM and aligned and x.dtype == w_gate_up.dtype
+            and x.dtype in SUPPORTED_DTYPES and H % 64 == 0 and (two_i // 2) % 64 == 0
+            and w_gate_up.stride(2) == 1 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
+            and w_gate_up.data_ptr() % 16 == 0):
+        tile = 128 if (two_i // 2) % 128 == 0 else 64
+        return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=tile)
+    if packed is not None and n * k > PACKED_MAX_ASSIGNMENTS:
+        packed = None  # the row kernel is faster there (see PACKED_MAX_ASSIGNMENTS)
+    sorted_ids, block_expert, num_valid = moe_align(topk_ids, E)
+    return moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, k,
                             num_splits=num_splits, packed=packed)

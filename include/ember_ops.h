@@ -442,6 +442,25 @@ int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, 
                             int64_t tokens, int64_t hidden, int64_t inter, int64_t column_tile, void* out,
                             int64_t out_row_stride, void* stream);
 
+/* The routed experts' gate_up projection with silu_and_mul as its epilogue at prefill sizes,
+ * replacing the first _grouped_gemm of fused_moe_forward and the silu_and_mul after it
+ * (emberserve/model/moe_triton.py:307-329, :339-340): the MFMA GEMM of
+ * ember_gate_up_silu_gemm over a block-aligned layout of 256-row blocks
+ * (ember_moe_align with block_m = 256: sorted_ids [num_blocks * 256], block_expert
+ * [num_blocks]). Block b multiplies the x rows sorted_ids[256 b + r] / top_k (entries >=
+ * num_valid are padding) by expert block_expert[b]'s W [2I, H] (at w + e * w_expert_stride,
+ * rows w_row_stride apart; blocks with an expert >= num_experts are skipped) and writes
+ * out[sorted_ids[256 b + r]] = silu(g) * u, rounded as ember_gate_up_silu does, for every
+ * real assignment: out [num_valid, inter] in assignment order, the `act` of
+ * moe_triton.py:340. Every accumulator runs over k in order, so a row's result is
+ * bit-identical to ember_moe_gate_up_silu's for the same assignment. column_tile 64 or 128
+ * (inter a multiple of it), hidden a multiple of 64, fp16/bf16, 16-byte aligned operands. */
+int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
+                                int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
+                                int64_t hidden, int64_t inter, const int32_t* sorted_ids,
+                                const int32_t* block_expert, int64_t num_blocks, int64_t num_valid, int64_t top_k,
+                                int64_t column_tile, void* out, int64_t out_row_stride, void* stream);
+
 /* The routed experts' gate_up + silu_and_mul over packed weights straight from the routing
  * ids, with no alignment: assignment a = token * top_k + choice (a < num_assignments,
  * topk_ids [num_assignments] int32 or int64 per id_bytes, row-major [tokens, top_k]) gets

@@ -16,8 +16,8 @@ if not torch.cuda.is_available():
     pytest.skip("needs a GPU", allow_module_level=True)
 
 from emberserve_amd import _lib  # noqa: E402
-from emberserve_amd.moe import (fused_moe_gate_up, moe_align, moe_gate_up_silu, moe_gate_up_silu_direct,  # noqa: E402
-                                pack_moe_gate_up_weight)
+from emberserve_amd.moe import (GEMM_FROM, fused_moe_gate_up, moe_align, moe_gate_up_silu,  # noqa: E402
+                                moe_gate_up_silu_direct, moe_gate_up_silu_gemm, pack_moe_gate_up_weight)
 from oracle import ref_ops as ref  # noqa: E402
 from tests.helpers import check_gate_up  # noqa: E402
 
@@ -184,3 +184,55 @@ def test_moe_direct_bad_expert_sets_error_bit():
     moe_gate_up_silu_direct(x.to(DEV), bad.to(DEV), pack_moe_gate_up_weight(dw))
     torch.cuda.synchronize()
     assert _lib.read_errors(clear=True) & _lib.ERR_EXPERT_ID
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 5, 37])
+def test_moe_gemm_matches_oracle(dtype, n):
+    """The prefill GEMM over 256-row blocks (mostly padding at these sizes) against the
+    oracle, at both column tiles."""
+    print(f"moe gemm n={n} {dtype}", flush=True)
+    x, w, ids = _inputs(n, dtype, seed=100 + n)
+    for tile in (64, 128):
+        got = moe_gate_up_silu_gemm(x.to(DEV), w.to(DEV), ids.to(DEV), column_tile=tile).cpu()
+        _check(got, x, w, ids, f"moe gemm n={n} tile {tile}")
+
+
+@pytest.mark.parametrize("n,experts,skew", [(300, 64, False), (700, 64, False), (600, 8, True)])
+def test_moe_gemm_equals_the_row_kernel(n, experts, skew):
+    """Bit-identical to the 16-block row kernel at one k split (every accumulator over k in
+    order): a few hundred tokens, runs spanning several 256-row blocks, and skewed routing
+    whose runs cross many blocks."""
+    print(f"moe gemm vs row n={n} E={experts} skew={skew}", flush=True)
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(n, H, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(experts, 2 * I, H, generator=g) * 1.5 / H ** 0.5).to(torch.bfloat16).to(DEV)
+    if skew:
+        ids = torch.stack([torch.randperm(experts, generator=g)[:K] for _ in range(n)])
+        ids[: n // 2] = torch.arange(K)  # half the tokens on experts 0-5
+    else:
+        ids = torch.stack([torch.randperm(experts, generator=g)[:K] for _ in range(n)])
+    ids = ids.to(DEV)
+    si, be, nv = moe_align(ids, experts)
+    want = moe_gate_up_silu(x, w, si, be, nv, K, num_splits=1)
+    for tile in (64, 128):
+        got = moe_gate_up_silu_gemm(x, w, ids, column_tile=tile)
+        assert torch.equal(got, want), tile
+
+
+def test_fused_moe_gate_up_takes_the_gemm_at_prefill_sizes(monkeypatch):
+    """From GEMM_FROM assignments fused_moe_gate_up runs the GEMM (bit-identical to the
+    row kernel at one split); below it the 16-block kernels."""
+    n = -(-GEMM_FROM // K)
+    x, w, ids = _inputs(n, torch.bfloat16, seed=9)
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    calls = []
+    import emberserve_amd.moe as moe_mod
+    real = moe_mod.moe_gate_up_silu_gemm
+    monkeypatch.setattr(moe_mod, "moe_gate_up_silu_gemm", lambda *a, **k: calls.append(1) or real(*a, **k))
+    got = fused_moe_gate_up(dx, dids, dw)
+    assert calls == [1]
+    si, be, nv = moe_align(dids, E)
+    assert torch.equal(got, moe_gate_up_silu(dx, dw, si, be, nv, K, num_splits=1))
+    fused_moe_gate_up(dx[:8], dids[:8], dw)
+    assert calls == [1]
