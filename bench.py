@@ -38,6 +38,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 PEAK_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
 METRIC = "achieved HBM GB/s (% of MI355X peak) per fused op; µs per layer at 7B"
 ROTATE_BYTES = 1.5 * 2 ** 30  # input sets rotated per op: > 5x the Infinity Cache
 
@@ -53,9 +54,10 @@ class Op:
     `cpu()` (optional) returns a zero-argument callable running the CPU oracle on the same
     shape (seeded inputs from oracle/inputs.py), for the per-row CPU timing."""
 
-    def __init__(self, name, config, shape, nbytes, make, run, footprint, cpu=None):
+    def __init__(self, name, config, shape, nbytes, make, run, footprint, cpu=None, flops=None):
         self.name, self.config, self.shape, self.nbytes = name, config, shape, nbytes
         self.make, self.run, self.footprint, self.cpu = make, run, footprint, cpu
+        self.flops = flops  # MFMA-bound rows: their matrix flops, reported against the bf16 peak
 
 
 _CPU_CACHE = {}
@@ -399,11 +401,13 @@ def _ops(torch, ops, tables):
             return (randn((t, hidden), bf, 370 + i), randn((2 * inter, hidden), bf, 380 + i, std=hidden ** -0.5))
         nbytes = wbytes + t * hidden * 2 + t * inter * 2
         shape = f"{label}: x[{t},{hidden}] w[{2 * inter},{hidden}] bf16"
+        flops = 2 * t * 2 * inter * hidden
         for tile in (64, 128):
             out.append(Op("gate_up_silu_gemm", cfg, shape + f" (MFMA GEMM, {tile}+{tile}-column tiles)", nbytes, make,
-                          lambda a, tile=tile: gate_up_silu_gemm(a[0], a[1], column_tile=tile), wbytes + t * hidden * 2))
+                          lambda a, tile=tile: gate_up_silu_gemm(a[0], a[1], column_tile=tile), wbytes + t * hidden * 2,
+                          flops=flops))
         out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
-                      lambda a: gate_up_silu_torch(a[0], a[1]), wbytes + t * hidden * 2))
+                      lambda a: gate_up_silu_torch(a[0], a[1]), wbytes + t * hidden * 2, flops=flops))
 
     def moe_gate_up(cfg, n):
         """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's
@@ -459,10 +463,11 @@ def _ops(torch, ops, tables):
         wbytes = ne * 2 * inter * h * 2
         nbytes = wbytes + n * h * 2 + n * k * inter * 2
         shape = f"moonlight: N={n} top-{k} of {ne} experts, w[{ne},{2 * inter},{h}] bf16"
+        flops = 2 * n * k * 2 * inter * h
         out.append(Op("moe_gate_up_silu_gemm", cfg, shape + " (align 256 + MFMA GEMM, 128-column tiles)", nbytes,
-                      make, lambda a: moe_gate_up_silu_gemm(a[0], a[1], ids, column_tile=128), wbytes))
+                      make, lambda a: moe_gate_up_silu_gemm(a[0], a[1], ids, column_tile=128), wbytes, flops=flops))
         out.append(Op("moe_align+gate_up_silu", cfg, shape + " (align 16 + 16-block kernel)", nbytes, make,
-                      lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes))
+                      lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes, flops=flops))
 
     def moe_align_row(cfg, n, ne=64, k=6):
         """ember_moe_align alone (moe_triton.py:215-254's layout in one launch): bytes are the
@@ -901,9 +906,15 @@ def main() -> int:
             _log(f"per-op: {op.name} cfg {op.config} {op.shape}")
             us, nsets = _time_op(torch, op, args.reps, max_sets=args.max_sets)
             gbps = op.nbytes / (us * 1e-6) / 1e9
+            if op.flops:
+                tf = op.flops / (us * 1e-6) / 1e12
+                _log(f"  {tf:.0f} TFLOP/s, {100 * tf / PEAK_BF16_TFLOPS:.1f}% of the dense bf16 MFMA peak")
             per_op.append({"op": op.name, "config": op.config, "shape": op.shape, "bytes": op.nbytes,
                            "us": round(us, 2), "GB/s": round(gbps, 1),
                            "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "input_sets": nsets})
+            if op.flops:
+                per_op[-1]["TFLOP/s"] = round(tf, 1)
+                per_op[-1]["pct_mfma"] = round(100 * tf / PEAK_BF16_TFLOPS, 1)
             cpu_rows.append((op, per_op[-1]))
             torch.cuda.empty_cache()
         if args.only:
@@ -1035,8 +1046,9 @@ def main() -> int:
     # short strings), so that every row survives a tail-limited capture of stdout.
     for r in per_op:
         cpu_s = f" cpu {r['cpu_GB/s']}GB/s" if "cpu_GB/s" in r else ""
+        mfma_s = f" {r['TFLOP/s']}TF {r['pct_mfma']}%mfma" if "TFLOP/s" in r else ""
         print(f"row cfg={r['config']} {r['op']} {r['shape']}: {r['us']}us {r['GB/s']}GB/s "
-              f"{r['pct_peak']}%{cpu_s}")
+              f"{r['pct_peak']}%{mfma_s}{cpu_s}")
     result["per_op"] = f"{len(per_op)} rows, printed above as 'row cfg=...' lines"
     print(json.dumps(result), flush=True)
     return 0
