@@ -449,11 +449,11 @@ def _ops(torch, ops, tables):
 
     def moe_prefill(cfg, n):
         """The routed experts' gate_up + silu_and_mul at prefill batches (Moonlight geometry):
-        what fused_moe_gate_up runs from 3072 assignments (moe_align over 256-row blocks + the
-        MFMA GEMM with the activation in its epilogue) beside the 16-block kernel of the
+        what fused_moe_gate_up runs from 1536 assignments (moe_align over 128- or 256-row
+        blocks + the MFMA GEMM with the activation in its epilogue) beside the 16-block kernel of the
         reference's structure (moe_triton.py:332-340: 16-row blocks of one expert). Alignment
         is launched in both. MFMA-bound: 2·N·k·2I·H flops; bytes as in the decode rows."""
-        from emberserve_amd.moe import moe_align, moe_gate_up_silu, moe_gate_up_silu_gemm
+        from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu
         h, inter, ne, k = 2048, 1408, 64, 6
         seed(350 + n)
         ids = torch.stack([torch.randperm(ne, generator=gi).to(dev)[:k] for _ in range(n)])
@@ -464,8 +464,9 @@ def _ops(torch, ops, tables):
         nbytes = wbytes + n * h * 2 + n * k * inter * 2
         shape = f"moonlight: N={n} top-{k} of {ne} experts, w[{ne},{2 * inter},{h}] bf16"
         flops = 2 * n * k * 2 * inter * h
-        out.append(Op("moe_gate_up_silu_gemm", cfg, shape + " (align 256 + MFMA GEMM, 128-column tiles)", nbytes,
-                      make, lambda a: moe_gate_up_silu_gemm(a[0], a[1], ids, column_tile=128), wbytes, flops=flops))
+        rows = 128 if n * k < 24576 else 256
+        out.append(Op("moe_gate_up_silu_gemm", cfg, shape + f" (fused_moe_gate_up: align {rows} + MFMA GEMM)", nbytes,
+                      make, lambda a: fused_moe_gate_up(a[0], ids, a[1]), wbytes, flops=flops))
         out.append(Op("moe_align+gate_up_silu", cfg, shape + " (align 16 + 16-block kernel)", nbytes, make,
                       lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes, flops=flops))
 

@@ -66,7 +66,6 @@ struct GemmMfma<__bf16> {
   }
 };
 
-constexpr int kGemmBM = 256;  // tokens per tile
 constexpr int kGemmRowB = 128;  // LDS row: 64 k of one operand row
 
 __device__ __forceinline__ void gemm_load_lds16(const void* gptr, void* lds_base) {
@@ -106,8 +105,8 @@ struct GemmArgs {
   void* out;
   int64_t os;
   int T, H, I;
-  // routed experts (MOE kernels only): token tiles are kGemmBM-assignment blocks of the
-  // block-aligned layout; block b's rows are assignments sorted_ids[b kGemmBM + r] (padding:
+  // routed experts (MOE kernels only): token tiles are BM-assignment blocks of the
+  // block-aligned layout; block b's rows are assignments sorted_ids[b BM + r] (padding:
   // >= num_valid) of expert block_expert[b], x row = assignment / top_k, output row = the
   // assignment; wes = elements between experts' [2I, H] weights
   const int32_t* sorted_ids;
@@ -116,31 +115,34 @@ struct GemmArgs {
   int64_t wes;
 };
 
-template <typename T, int BNG, bool MOE>
+template <typename T, int BNG, int BM, bool MOE>
 __global__ void __launch_bounds__(512, 1)
 k_gate_up_silu_gemm(GemmArgs a) {
   using M = GemmMfma<T>;
   using V8 = typename M::v8;
-  static_assert(BNG == 64 || BNG == 128, "column tile");
-  constexpr int NT = BNG / 16;                 // row tiles per wave: NT / 2 gate, NT / 2 up
+  static_assert((BM == 256 && (BNG == 64 || BNG == 128)) || (BM == 128 && BNG == 128), "tile");
+  constexpr int TG = BM / 64;                  // token groups of 64
+  constexpr int WC = BNG * TG / 8;             // gate (and up) columns per wave
+  constexpr int NT = 2 * WC / 16;              // row tiles per wave: NT / 2 gate, NT / 2 up
   constexpr int WREG = 2 * BNG * kGemmRowB;    // weight region of a double stage
-  constexpr int XREG = kGemmBM * kGemmRowB;    // x region
+  constexpr int XREG = BM * kGemmRowB;         // x region
   constexpr int DST = WREG + XREG;             // one double stage (64 k)
-  constexpr int LOADS = (2 * BNG + kGemmBM) / 8 / 8;  // 1 KiB load instructions per wave per double stage
+  constexpr int LOADS = (2 * BNG + BM) / 8 / 8;  // 1 KiB load instructions per wave per double stage
   // Double-stage buffers: NBUF - 1 double stages of loads in flight while one is consumed.
-  constexpr int NBUF = BNG == 64 ? EMBER_GEMM_NBUF64 : 2;
+  constexpr int NBUF = 3 * DST <= 160 * 1024 ? EMBER_GEMM_NBUF64 : 2;
   static_assert(NBUF * DST <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[NBUF * DST];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = w >> 2;
-  const int q = w & 3;
+  const int grp = w >> 2;    // ping-pong group: waves w and w + 4 share a SIMD
+  const int q = w % TG;      // token group
+  const int cg = w / TG;     // column group
   const int n = lane & 15, g = lane >> 4;
 
   // XCD-aware tile order, then GROUP_M token tiles per band of column tiles
-  const int mtiles = (a.T + kGemmBM - 1) / kGemmBM;
+  const int mtiles = (a.T + BM - 1) / BM;
   const int ntiles = a.I / BNG;
   int pid = blockIdx.x;
   {
@@ -156,7 +158,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
   const int gsize = min(mtiles - first_m, GM);
   const int mt = first_m + (pid % (GM * ntiles)) % gsize;
   const int nt = (pid % (GM * ntiles)) / gsize;
-  const int m0 = mt * kGemmBM, n0 = nt * BNG;
+  const int m0 = mt * BM, n0 = nt * BNG;
 
   const T* X = static_cast<const T*>(a.x);
   const T* W = static_cast<const T*>(a.w);
@@ -201,7 +203,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
   int woff[NT], xoff[4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
-    woff[t] = ((t < NT / 2 ? 0 : BNG) + (BNG / 2) * grp + 16 * (t % (NT / 2)) + n) * kGemmRowB;
+    woff[t] = ((t < NT / 2 ? 0 : BNG) + WC * cg + 16 * (t % (NT / 2)) + n) * kGemmRowB;
 #pragma unroll
   for (int u = 0; u < 4; ++u) xoff[u] = WREG + (64 * q + 16 * u + n) * kGemmRowB;
   const int sw = n & 7;  // row % 8 of every fragment row
@@ -263,7 +265,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
     if (real) {
 #pragma unroll
       for (int t = 0; t < NT / 2; ++t) {
-        const int col = n0 + (BNG / 2) * grp + 16 * t + 4 * g;
+        const int col = n0 + WC * cg + 16 * t + 4 * g;
         Pack<T, 4> o;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -278,24 +280,36 @@ k_gate_up_silu_gemm(GemmArgs a) {
   }
 }
 
-template <typename T, int BNG, bool MOE = false>
+template <typename T, int BNG, int BM = 256, bool MOE = false>
 int launch_gemm(const GemmArgs& a, hipStream_t st) {
-  const int64_t grid = cdiv(a.T, kGemmBM) * (a.I / BNG);
+  const int64_t grid = cdiv(a.T, BM) * (a.I / BNG);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, MOE>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
+  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, BM, MOE>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
   return launch_status();
+}
+
+// The tile shapes: (tokens, gate columns) of 256 x 64, 256 x 128 or 128 x 128; every one
+// gives each of the 8 waves 64 tokens x (WC gate + WC up) columns.
+template <typename T, bool MOE>
+int launch_tile(const GemmArgs& a, int64_t token_tile, int64_t column_tile, hipStream_t st) {
+  if (token_tile == 128) return launch_gemm<T, 128, 128, MOE>(a, st);
+  return column_tile == 64 ? launch_gemm<T, 64, 256, MOE>(a, st) : launch_gemm<T, 128, 256, MOE>(a, st);
+}
+
+bool gemm_tile_ok(int64_t token_tile, int64_t column_tile) {
+  return (token_tile == 256 && (column_tile == 64 || column_tile == 128)) || (token_tile == 128 && column_tile == 128);
 }
 
 }  // namespace
 }  // namespace ember
 
 extern "C" int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
-                                       int dtype, int64_t tokens, int64_t hidden, int64_t inter,
+                                       int dtype, int64_t tokens, int64_t hidden, int64_t inter, int64_t token_tile,
                                        int64_t column_tile, void* out, int64_t out_row_stride, void* stream) {
   using namespace ember;
   if (tokens == 0) return EMBER_OK;
   if (tokens < 0 || tokens > (int64_t(1) << 24) || hidden < 64 || hidden % 64 != 0 || hidden > (int64_t(1) << 20) ||
-      (column_tile != 64 && column_tile != 128) || inter < column_tile || inter % column_tile != 0 ||
+      !gemm_tile_ok(token_tile, column_tile) || inter < column_tile || inter % column_tile != 0 ||
       inter > (int64_t(1) << 28))
     return EMBER_EINVAL;
   if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
@@ -307,22 +321,21 @@ extern "C" int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, cons
   GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(tokens),
              static_cast<int>(hidden), static_cast<int>(inter), nullptr, nullptr, 0, 1, 0, 0, 0};
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == EMBER_F16)
-    return column_tile == 64 ? launch_gemm<_Float16, 64>(a, st) : launch_gemm<_Float16, 128>(a, st);
-  return column_tile == 64 ? launch_gemm<__bf16, 64>(a, st) : launch_gemm<__bf16, 128>(a, st);
+  if (dtype == EMBER_F16) return launch_tile<_Float16, false>(a, token_tile, column_tile, st);
+  return launch_tile<__bf16, false>(a, token_tile, column_tile, st);
 }
 
 extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
                                            int64_t w_expert_stride, int64_t w_row_stride, int dtype,
                                            int64_t num_experts, int64_t hidden, int64_t inter,
                                            const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
-                                           int64_t num_valid, int64_t top_k, int64_t column_tile, void* out,
-                                           int64_t out_row_stride, void* stream) {
+                                           int64_t block_rows, int64_t num_valid, int64_t top_k, int64_t column_tile,
+                                           void* out, int64_t out_row_stride, void* stream) {
   using namespace ember;
   if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
   if (num_blocks < 0 || num_valid < 0 || num_tokens < 1 || top_k < 1 || num_experts < 1 || num_blocks > (1 << 22) ||
       num_valid > INT32_MAX / 2 || num_tokens > INT32_MAX || hidden < 64 || hidden % 64 != 0 ||
-      hidden > (int64_t(1) << 20) || (column_tile != 64 && column_tile != 128) || inter < column_tile ||
+      hidden > (int64_t(1) << 20) || !gemm_tile_ok(block_rows, column_tile) || inter < column_tile ||
       inter % column_tile != 0 || inter > (int64_t(1) << 28))
     return EMBER_EINVAL;
   if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
@@ -333,12 +346,11 @@ extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, 
       out_row_stride < inter || x_row_stride % 8 != 0 || w_row_stride % 8 != 0 || w_expert_stride % 8 != 0 ||
       out_row_stride % 4 != 0)
     return EMBER_EINVAL;
-  GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(num_blocks * kGemmBM),
+  GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(num_blocks * block_rows),
              static_cast<int>(hidden), static_cast<int>(inter), sorted_ids, block_expert,
              static_cast<int>(num_valid), static_cast<int>(top_k), static_cast<int>(num_experts),
              static_cast<int>(num_tokens), w_expert_stride};
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == EMBER_F16)
-    return column_tile == 64 ? launch_gemm<_Float16, 64, true>(a, st) : launch_gemm<_Float16, 128, true>(a, st);
-  return column_tile == 64 ? launch_gemm<__bf16, 64, true>(a, st) : launch_gemm<__bf16, 128, true>(a, st);
+  if (dtype == EMBER_F16) return launch_tile<_Float16, true>(a, block_rows, column_tile, st);
+  return launch_tile<__bf16, true>(a, block_rows, column_tile, st);
 }

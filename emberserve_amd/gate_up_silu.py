@@ -133,10 +133,11 @@ def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> Pa
     return PackedGateUp(packed, H, I, programs)
 
 
-def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128) -> Tensor:
+def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128, token_tile: int = 256) -> Tensor:
     """silu_and_mul(F.linear(x, weight)) as one MFMA GEMM whose epilogue applies the
-    activation (`ember_gate_up_silu_gemm`): 256-token x (column_tile gate + column_tile up)
-    tiles, any token count. Needs fp16/bf16, H a multiple of 64, I of column_tile."""
+    activation (`ember_gate_up_silu_gemm`): token_tile x (column_tile gate + column_tile up)
+    tiles ((256, 64), (256, 128) or (128, 128)), any token count. Needs fp16/bf16, H a
+    multiple of 64, I of column_tile."""
     if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
         raise ValueError(f"gate_up_silu_gemm: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
                          "a [2I, H] gate_up projection")
@@ -148,12 +149,13 @@ def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128) -> T
     out = torch.empty((T, I), dtype=x.dtype, device=x.device)
     if T == 0:
         return out.view(*x.shape[:-1], I)
-    if not (_fits(x2, weight, out, max_tokens=1 << 24) and I % column_tile == 0):
+    if not (_fits(x2, weight, out, max_tokens=1 << 24) and I % column_tile == 0
+            and (token_tile, column_tile) in ((256, 64), (256, 128), (128, 128))):
         raise ValueError(f"gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {I}, "
                          f"column_tile {column_tile}, {x.dtype})")
     _launch("ember_gate_up_silu_gemm", _lib.load().ember_gate_up_silu_gemm, x.device,
             x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
-            T, H, I, column_tile, out.data_ptr(), out.stride(0))
+            T, H, I, token_tile, column_tile, out.data_ptr(), out.stride(0))
     return out.view(*x.shape[:-1], I)
 
 

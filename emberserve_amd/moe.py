@@ -243,18 +243,23 @@ def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_exp
 
 
 GEMM_BLOCK_M = 256  # rows per block of the prefill GEMM's layout (its token tile)
-# fused_moe_gate_up: the GEMM from this many assignments, the packed 16-block kernel up to
+# fused_moe_gate_up: the GEMM from GEMM_FROM assignments (128-row blocks below
+# GEMM_WIDE_FROM, 256-row ones from there), the packed 16-block kernel up to
 # PACKED_MAX_ASSIGNMENTS. Measured at Moonlight's geometry (bf16, µs, alignment included;
-# row kernel at its default splits | GEMM at 128-column tiles): 384 assignments 147 | 207,
-# 1536: 223 | 255, 3072: 292 | 272, 6144: 494 | 272, 12288: 823 | 330, 49152: 2727 | 673.
-# The packed kernel: 384 assignments 115 against the row kernel's 136; 1536: 228 against 205.
-GEMM_FROM = 3072
+# row kernel at its default splits | GEMM 256 x 128 | GEMM 128 x 128): 1536 assignments
+# 226 | 259 | 200, 3072: 291 | 292 | 204, 6144: 499 | 282 | 243, 12288: 840 | 341 | 294,
+# 49152: 2722 | 688 | 736. The packed kernel: 384 assignments 115 against the row
+# kernel's 136; 1536: 228 against 205.
+GEMM_FROM = 1536
+GEMM_WIDE_FROM = 24576
 PACKED_MAX_ASSIGNMENTS = 768
 
 
-def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, column_tile: int = 128) -> Tensor:
+def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, column_tile: int = 128,
+                          block_rows: int = GEMM_BLOCK_M) -> Tensor:
     """act [N * k, I] at prefill sizes (`ember_moe_gate_up_silu_gemm`): moe_align with
-    256-row blocks, then the MFMA GEMM of `gate_up_silu_gemm` over each block's gathered x
+    block_rows-row blocks (256, or 128 with 128-column tiles), then the MFMA GEMM of
+    `gate_up_silu_gemm` with one block per token tile over the block's gathered x
     rows and its expert's weight, silu_and_mul in the epilogue, rows scattered back to
     assignment order. The first grouped GEMM + silu_and_mul of moe_triton.py:339-340;
     bit-identical to `moe_gate_up_silu` for every assignment."""
@@ -266,7 +271,9 @@ def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, col
     if x.shape[1] != H or two_i % 2 or n > x.shape[0]:
         raise ValueError(f"moe_gate_up_silu_gemm: x {tuple(x.shape)}, w_gate_up {tuple(w_gate_up.shape)} and "
                          f"topk_ids {tuple(topk_ids.shape)} do not match")
-    sorted_ids, block_expert, num_valid = moe_align(topk_ids, E, GEMM_BLOCK_M)
+    if (block_rows, column_tile) not in ((256, 64), (256, 128), (128, 128)):
+        raise ValueError(f"moe_gate_up_silu_gemm: no ({block_rows}, {column_tile}) tile")
+    sorted_ids, block_expert, num_valid = moe_align(topk_ids, E, block_rows)
     out = torch.empty((num_valid, inter), dtype=x.dtype, device=x.device)
     if num_valid == 0:
         return out
@@ -280,7 +287,7 @@ def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, col
     _launch("ember_moe_gate_up_silu_gemm", _lib.load().ember_moe_gate_up_silu_gemm, x.device,
             x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
             _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
-            block_expert.numel(), num_valid, k, column_tile, out.data_ptr(), out.stride(0))
+            block_expert.numel(), block_rows, num_valid, k, column_tile, out.data_ptr(), out.stride(0))
     return out
 
 
@@ -327,8 +334,10 @@ def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_spl
             and x.dtype in SUPPORTED_DTYPES and H % 64 == 0 and (two_i // 2) % 64 == 0
             and w_gate_up.stride(2) == 1 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
             and w_gate_up.data_ptr() % 16 == 0):
-        tile = 128 if (two_i // 2) % 128 == 0 else 64
-        return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=tile)
+        if (two_i // 2) % 128 == 0:
+            rows = 128 if n * k < GEMM_WIDE_FROM else 256
+            return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=128, block_rows=rows)
+        return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=64, block_rows=256)
     if packed is not None and n * k > PACKED_MAX_ASSIGNMENTS:
         packed = None  # the row kernel is faster there (see PACKED_MAX_ASSIGNMENTS)
     sorted_ids, block_expert, num_valid = moe_align(topk_ids, E)

@@ -430,36 +430,39 @@ int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t n
                                   void* workspace, int64_t workspace_bytes, void* out, int64_t out_row_stride,
                                   void* stream);
 
-/* The gate_up projection + silu_and_mul at prefill sizes: an MFMA GEMM over 256-token x
+/* The gate_up projection + silu_and_mul at prefill sizes: an MFMA GEMM over token_tile x
  * (column_tile gate + column_tile up) tiles whose epilogue applies silu_and_mul, writing only
  * out [tokens, inter] (out[t, j] = round(round(silu(g)) * u), g and u the dot products
  * rounded to the dtype). x [tokens, hidden], w [2 inter, hidden] (gate rows, then up rows),
  * fp16 or bf16, 16-byte aligned, unit inner stride; hidden a multiple of 64, inter of
- * column_tile (64 or 128). No workspace. Each accumulator runs over k in order in one chain,
+ * column_tile. Tiles (token_tile, column_tile): (256, 64), (256, 128) or (128, 128). No
+ * workspace. Each accumulator runs over k in order in one chain,
  * so a token's result equals ember_gate_up_silu_packed's over whole-slab runs bit for bit.
  * Replaces qwen2.py:60-61 (gate_up_proj, then silu_and_mul) without the [T, 2I] round trip. */
 int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
-                            int64_t tokens, int64_t hidden, int64_t inter, int64_t column_tile, void* out,
-                            int64_t out_row_stride, void* stream);
+                            int64_t tokens, int64_t hidden, int64_t inter, int64_t token_tile, int64_t column_tile,
+                            void* out, int64_t out_row_stride, void* stream);
 
 /* The routed experts' gate_up projection with silu_and_mul as its epilogue at prefill sizes,
  * replacing the first _grouped_gemm of fused_moe_forward and the silu_and_mul after it
  * (emberserve/model/moe_triton.py:307-329, :339-340): the MFMA GEMM of
- * ember_gate_up_silu_gemm over a block-aligned layout of 256-row blocks
- * (ember_moe_align with block_m = 256: sorted_ids [num_blocks * 256], block_expert
- * [num_blocks]). Block b multiplies the x rows sorted_ids[256 b + r] / top_k (entries >=
- * num_valid are padding) by expert block_expert[b]'s W [2I, H] (at w + e * w_expert_stride,
- * rows w_row_stride apart; blocks with an expert >= num_experts are skipped) and writes
- * out[sorted_ids[256 b + r]] = silu(g) * u, rounded as ember_gate_up_silu does, for every
- * real assignment: out [num_valid, inter] in assignment order, the `act` of
- * moe_triton.py:340. Every accumulator runs over k in order, so a row's result is
- * bit-identical to ember_moe_gate_up_silu's for the same assignment. column_tile 64 or 128
- * (inter a multiple of it), hidden a multiple of 64, fp16/bf16, 16-byte aligned operands. */
+ * ember_gate_up_silu_gemm over a block-aligned layout of block_rows-row blocks
+ * (ember_moe_align with block_m = block_rows: sorted_ids [num_blocks * block_rows],
+ * block_expert [num_blocks]), one block per token tile. Block b multiplies the x rows
+ * sorted_ids[block_rows b + r] / top_k (entries >= num_valid are padding) by expert
+ * block_expert[b]'s W [2I, H] (at w + e * w_expert_stride, rows w_row_stride apart; blocks
+ * with an expert >= num_experts are skipped) and writes out[sorted_ids[block_rows b + r]] =
+ * silu(g) * u, rounded as ember_gate_up_silu does, for every real assignment: out
+ * [num_valid, inter] in assignment order, the `act` of moe_triton.py:340. Every accumulator
+ * runs over k in order, so a row's result is bit-identical to ember_moe_gate_up_silu's for
+ * the same assignment. (block_rows, column_tile) as ember_gate_up_silu_gemm's tiles; inter a
+ * multiple of column_tile, hidden of 64, fp16/bf16, 16-byte aligned operands. */
 int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* w,
                                 int64_t w_expert_stride, int64_t w_row_stride, int dtype, int64_t num_experts,
                                 int64_t hidden, int64_t inter, const int32_t* sorted_ids,
-                                const int32_t* block_expert, int64_t num_blocks, int64_t num_valid, int64_t top_k,
-                                int64_t column_tile, void* out, int64_t out_row_stride, void* stream);
+                                const int32_t* block_expert, int64_t num_blocks, int64_t block_rows,
+                                int64_t num_valid, int64_t top_k, int64_t column_tile, void* out,
+                                int64_t out_row_stride, void* stream);
 
 /* The routed experts' gate_up + silu_and_mul over packed weights straight from the routing
  * ids, with no alignment: assignment a = token * top_k + choice (a < num_assignments,

@@ -234,18 +234,18 @@ def test_swiglu_mlp_packed_weights():
 
 
 # ---- prefill sizes: the MFMA GEMM with the activation as its epilogue ----
-@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("token_tile,tile", [(256, 64), (256, 128), (128, 128)])
 @pytest.mark.parametrize("tokens", [1, 16, 64, 300])
-def test_gemm_equals_the_packed_kernel(tile, tokens):
+def test_gemm_equals_the_packed_kernel(token_tile, tile, tokens):
     """Every accumulator runs over k in order in one chain, as the packed kernel's over
     whole-slab runs (76 workgroups for Qwen2.5-0.5B's 76 slabs): bit-identical per token,
     in 64-token chunks past 64 (token tiles padded, a partial last tile)."""
     from emberserve_amd.gate_up_silu import gate_up_silu_gemm, pack_gate_up_weight
-    _say(f"gemm gate_up tile={tile} T={tokens}")
+    _say(f"gemm gate_up tile={token_tile}x{tile} T={tokens}")
     g = torch.Generator().manual_seed(900 + tokens)
     x = (torch.randn(tokens, 896, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
     w = (torch.randn(2 * 4864, 896, generator=g) / 896 ** 0.5).to(torch.bfloat16).to(DEV)
-    got = gate_up_silu_gemm(x, w, column_tile=tile)
+    got = gate_up_silu_gemm(x, w, column_tile=tile, token_tile=token_tile)
     packed = pack_gate_up_weight(w, 76)
     for t0 in range(0, tokens, 64):
         want = gate_up_silu(x[t0:t0 + 64], w, fused=True, packed=packed)

@@ -383,13 +383,13 @@ def test_moe_align_workspace_and_abi_validation():
 def test_moe_gate_up_silu_gemm_abi_validation():
     lib = _lib.load()
 
-    def call(blocks=4, valid=10, tokens=5, top_k=2, experts=8, hidden=2048, inter=1408, tile=64, dtype=2):
+    def call(blocks=4, rows=256, valid=10, tokens=5, top_k=2, experts=8, hidden=2048, inter=1408, tile=64, dtype=2):
         return lib.ember_moe_gate_up_silu_gemm(None, hidden, tokens, None, 2 * inter * hidden, hidden, dtype, experts,
-                                               hidden, inter, None, None, blocks, valid, top_k, tile, None, inter,
-                                               None)
+                                               hidden, inter, None, None, blocks, rows, valid, top_k, tile, None,
+                                               inter, None)
     assert call(blocks=0) == 0 and call(valid=0) == 0  # nothing to do
-    for bad in (dict(tokens=0), dict(top_k=0), dict(experts=0), dict(hidden=100), dict(tile=32), dict(tile=128, inter=1344),
-                dict(dtype=0)):
+    for bad in (dict(tokens=0), dict(top_k=0), dict(experts=0), dict(hidden=100), dict(tile=32),
+                dict(tile=128, inter=1344), dict(rows=128), dict(rows=64, tile=128), dict(dtype=0)):
         assert call(**bad) == 1, bad
     assert call() == 1  # null pointers
 

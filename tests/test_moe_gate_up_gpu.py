@@ -193,9 +193,9 @@ def test_moe_gemm_matches_oracle(dtype, n):
     oracle, at both column tiles."""
     print(f"moe gemm n={n} {dtype}", flush=True)
     x, w, ids = _inputs(n, dtype, seed=100 + n)
-    for tile in (64, 128):
-        got = moe_gate_up_silu_gemm(x.to(DEV), w.to(DEV), ids.to(DEV), column_tile=tile).cpu()
-        _check(got, x, w, ids, f"moe gemm n={n} tile {tile}")
+    for rows, tile in ((256, 64), (256, 128), (128, 128)):
+        got = moe_gate_up_silu_gemm(x.to(DEV), w.to(DEV), ids.to(DEV), column_tile=tile, block_rows=rows).cpu()
+        _check(got, x, w, ids, f"moe gemm n={n} tile {rows}x{tile}")
 
 
 @pytest.mark.parametrize("n,experts,skew", [(300, 64, False), (700, 64, False), (600, 8, True)])
@@ -215,9 +215,9 @@ def test_moe_gemm_equals_the_row_kernel(n, experts, skew):
     ids = ids.to(DEV)
     si, be, nv = moe_align(ids, experts)
     want = moe_gate_up_silu(x, w, si, be, nv, K, num_splits=1)
-    for tile in (64, 128):
-        got = moe_gate_up_silu_gemm(x, w, ids, column_tile=tile)
-        assert torch.equal(got, want), tile
+    for rows, tile in ((256, 64), (256, 128), (128, 128)):
+        got = moe_gate_up_silu_gemm(x, w, ids, column_tile=tile, block_rows=rows)
+        assert torch.equal(got, want), (rows, tile)
 
 
 def test_fused_moe_gate_up_takes_the_gemm_at_prefill_sizes(monkeypatch):
