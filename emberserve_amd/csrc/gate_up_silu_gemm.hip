@@ -12,7 +12,9 @@
 //     BNG/2 grp .. BNG/2 grp + BNG/2 - 1 of both the gate and the up half, so it holds
 //     (BNG / 16) x 4 accumulator tiles of 16 x 16;
 //   * the tile's operands stream through an LDS ring of "double stages" of 64 k (three for
-//     the 64-column tile, two for the 128-column one, which fill 128 KiB): rows of 128
+//     the 256 x 64 and 128 x 128 tiles; for 256 x 128, where three would not fit, separate
+//     rings of three weight and two x buffers, 160 KiB: 94 instead of 102 us for Qwen3-8B
+//     at 256 tokens, the same at 8192): rows of 128
 //     bytes (one 64-k line per row), so each direct-to-LDS load (global_load_lds_dwordx4)
 //     moves 8 rows x 128 B; 16-byte chunks XOR-swizzled by row & 7 so the fragment reads
 //     (one row per lane) spread over the banks. At 256 tokens each workgroup streams its
@@ -40,6 +42,9 @@
 #define EMBER_GEMM_GROUP_M 8
 #endif
 // Double-stage buffers of the 64-column tile (the 128-column tile's two fill 128 KiB).
+#ifndef EMBER_GEMM_SPLIT_RING
+#define EMBER_GEMM_SPLIT_RING 1
+#endif
 #ifndef EMBER_GEMM_NBUF64
 #define EMBER_GEMM_NBUF64 3
 #endif
@@ -130,8 +135,14 @@ k_gate_up_silu_gemm(GemmArgs a) {
   constexpr int LOADS = (2 * BNG + BM) / 8 / 8;  // 1 KiB load instructions per wave per double stage
   // Double-stage buffers: NBUF - 1 double stages of loads in flight while one is consumed.
   constexpr int NBUF = 3 * DST <= 160 * 1024 ? EMBER_GEMM_NBUF64 : 2;
-  static_assert(NBUF * DST <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[NBUF * DST];
+  // SPLIT: when three double stages do not fit, the operands get rings of their own: three
+  // weight buffers (HBM latency) and two x buffers (mostly L2 hits), 160 KiB in all. Each
+  // wave then loads WL weight blocks and LOADS - WL x blocks per double stage.
+  constexpr bool SPLIT = EMBER_GEMM_SPLIT_RING != 0 && NBUF == 2 && 3 * WREG + 2 * XREG <= 160 * 1024;
+  constexpr int WL = SPLIT ? 2 * BNG / 8 / 8 : 0;
+  constexpr int LDS_BYTES = SPLIT ? 3 * WREG + 2 * XREG : NBUF * DST;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -172,40 +183,61 @@ k_gate_up_silu_gemm(GemmArgs a) {
   // loads 16-byte chunk (l % 8) ^ (row % 8) of its row into slot l of the 1 KiB block.
   const T* src[LOADS];
   int dst[LOADS];
+  auto x_src = [&](int xr, int c) {
+    int64_t xrow;
+    if (MOE) {  // padding assignments read token 0 and store nothing
+      const int id = a.sorted_ids[m0 + xr];
+      xrow = id >= 0 && id < a.num_valid ? min(id / a.top_k, a.ntok - 1) : 0;
+    } else {
+      xrow = min(m0 + xr, a.T - 1);  // padded tokens: the last real one
+    }
+    return X + xrow * a.xs + 8 * c;
+  };
+  auto w_src = [&](int row, int c) {
+    const int wr = row < BNG ? n0 + row : a.I + n0 + (row - BNG);
+    return W + static_cast<int64_t>(wr) * a.ws + 8 * c;
+  };
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
-    const int ins = LOADS * w + i;  // 0 .. 2 BNG / 8 + 31
-    const int row = 8 * ins + (lane >> 3);
-    const int c = (lane & 7) ^ (row & 7);
-    if (row < 2 * BNG) {
-      const int wr = row < BNG ? n0 + row : a.I + n0 + (row - BNG);
-      src[i] = W + static_cast<int64_t>(wr) * a.ws + 8 * c;
+    if (SPLIT) {  // block offsets within the operand's own buffer
+      const int ins = i < WL ? WL * w + i : (LOADS - WL) * w + (i - WL);
+      const int row = 8 * ins + (lane >> 3);
+      const int c = (lane & 7) ^ (row & 7);
+      src[i] = i < WL ? w_src(row, c) : x_src(row, c);
+      dst[i] = ins * 1024;
     } else {
-      const int xr = row - 2 * BNG;
-      int64_t xrow;
-      if (MOE) {  // padding assignments read token 0 and store nothing
-        const int id = a.sorted_ids[m0 + xr];
-        xrow = id >= 0 && id < a.num_valid ? min(id / a.top_k, a.ntok - 1) : 0;
-      } else {
-        xrow = min(m0 + xr, a.T - 1);  // padded tokens: the last real one
-      }
-      src[i] = X + xrow * a.xs + 8 * c;
+      const int ins = LOADS * w + i;  // 0 .. 2 BNG / 8 + BM / 8 - 1
+      const int row = 8 * ins + (lane >> 3);
+      const int c = (lane & 7) ^ (row & 7);
+      src[i] = row < 2 * BNG ? w_src(row, c) : x_src(row - 2 * BNG, c);
+      dst[i] = ins * 1024;  // the weight region is rows 0 .. 2 BNG - 1, the x region follows
     }
-    dst[i] = ins * 1024;  // the weight region is rows 0 .. 2 BNG - 1, the x region follows
   }
   const int nd = a.H / 64;  // double stages
+  auto wbuf = [&](int d) { return lds + (SPLIT ? (d % 3) * WREG : (d % NBUF) * DST); };
+  auto xbuf = [&](int d) { return lds + (SPLIT ? 3 * WREG + (d % 2) * XREG : (d % NBUF) * DST + WREG); };
   auto issue = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
     unsigned char* st = lds + (d % NBUF) * DST;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) gemm_load_lds16(src[i] + kk, st + dst[i]);
   };
+  auto issue_w = [&](int d) {
+    const int kk = min(d, nd - 1) * 64;
+#pragma unroll
+    for (int i = 0; i < WL; ++i) gemm_load_lds16(src[i] + kk, wbuf(d) + dst[i]);
+  };
+  auto issue_x = [&](int d) {
+    const int kk = min(d, nd - 1) * 64;
+#pragma unroll
+    for (int i = WL; i < LOADS; ++i) gemm_load_lds16(src[i] + kk, xbuf(d) + dst[i]);
+  };
   int woff[NT], xoff[4];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
     woff[t] = ((t < NT / 2 ? 0 : BNG) + WC * cg + 16 * (t % (NT / 2)) + n) * kGemmRowB;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) xoff[u] = WREG + (64 * q + 16 * u + n) * kGemmRowB;
+  for (int u = 0; u < 4; ++u) xoff[u] = (64 * q + 16 * u + n) * kGemmRowB;
   const int sw = n & 7;  // row % 8 of every fragment row
 
   f32x4 acc[NT][4];
@@ -215,21 +247,39 @@ k_gate_up_silu_gemm(GemmArgs a) {
     for (int u = 0; u < 4; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
   V8 fw[NT], fx[4];
 
+  // vmcnt after which the next double stage has landed: split rings issue x(j + 1), then
+  // w(j + 2) at each even step, so all but the last WL loads
+  constexpr int kNextLanded = SPLIT ? WL : (NBUF - 2) * LOADS;
+  if (SPLIT) {
+    issue_w(0);
+    issue_x(0);
+    issue_w(1);
+  } else {
 #pragma unroll
-  for (int d = 0; d < NBUF - 1; ++d) issue(d);
-  gemm_wait_vm<(NBUF - 2) * LOADS>();
+    for (int d = 0; d < NBUF - 1; ++d) issue(d);
+  }
+  gemm_wait_vm<kNextLanded>();
   gemm_barrier();
-  // M(s): at an even 32-k stage issue the next double stage's loads into the other buffer;
-  // read this stage's fragments; at an odd stage wait for the next double stage's loads.
+  // M(s): at an even 32-k stage issue the next loads into free buffers; read this stage's
+  // fragments; at an odd stage wait for the next double stage's loads.
   auto mphase = [&](int s, bool even) {
-    if (even) issue(s / 2 + NBUF - 1);
-    const unsigned char* st = lds + ((s >> 1) % NBUF) * DST;
+    const int j = s >> 1;
+    if (even) {
+      if (SPLIT) {
+        issue_x(j + 1);
+        issue_w(j + 2);
+      } else {
+        issue(j + NBUF - 1);
+      }
+    }
+    const unsigned char* sw_ = wbuf(j);
+    const unsigned char* sx_ = xbuf(j);
     const int co = ((4 * (s & 1) + g) ^ sw) << 4;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) fw[t] = *reinterpret_cast<const V8*>(st + woff[t] + co);
+    for (int t = 0; t < NT; ++t) fw[t] = *reinterpret_cast<const V8*>(sw_ + woff[t] + co);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) fx[u] = *reinterpret_cast<const V8*>(st + xoff[u] + co);
-    if (!even) gemm_wait_vm<(NBUF - 2) * LOADS>();  // the next double stage has landed
+    for (int u = 0; u < 4; ++u) fx[u] = *reinterpret_cast<const V8*>(sx_ + xoff[u] + co);
+    if (!even) gemm_wait_vm<kNextLanded>();  // the next double stage has landed
     gemm_wait_lgkm0();
   };
   auto cphase = [&]() {
