@@ -277,11 +277,13 @@ def test_gemm_rejects_bad_tiles():
 
 def test_fused_true_past_64_tokens_runs_the_gemm():
     """gate_up_silu(..., fused=True) above the decode kernels' limit is the GEMM (64-column
-    tiles up to 512 tokens, 128 above); the default keeps the unfused pair."""
+    tiles while they fit one round on the CUs, else 128); the default keeps the unfused pair."""
     from emberserve_amd.gate_up_silu import gate_up_silu_gemm
     g = torch.Generator().manual_seed(77)
     w = (torch.randn(2 * 256, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
-    for tokens, tile in ((100, 64), (600, 128)):
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    many = 256 * (cus // 4 + 1)  # more 256 x 64 tiles (4 per 256 tokens here) than CUs
+    for tokens, tile in ((100, 64), (600, 64), (many, 128)):
         x = (torch.randn(tokens, 512, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
         assert torch.equal(gate_up_silu(x, w, fused=True), gate_up_silu_gemm(x, w, column_tile=tile))
         assert torch.equal(gate_up_silu(x, w), gate_up_silu_torch(x, w))

@@ -380,6 +380,17 @@ def test_moe_align_workspace_and_abi_validation():
     assert call() == 1  # null pointers
 
 
+def test_gemm_column_tile_rule(monkeypatch):
+    """64-column tiles while 256-token x 64-column tiles fit one round on the CUs."""
+    import emberserve_amd.gate_up_silu as gu
+    monkeypatch.setattr(gu, "num_sms", lambda device: 256)
+    dev = torch.device("cpu")
+    assert gu.gemm_column_tile(256, 12288, dev) == 64      # Qwen3-8B: 192 tiles
+    assert gu.gemm_column_tile(256, 18944, dev) == 128     # Qwen2.5-7B: 296 tiles
+    assert gu.gemm_column_tile(1024, 12288, dev) == 128
+    assert gu.gemm_column_tile(8192, 4864 + 64, dev) == 64  # 128 does not divide inter
+
+
 def test_moe_gate_up_silu_gemm_abi_validation():
     lib = _lib.load()
 
