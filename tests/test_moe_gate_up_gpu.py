@@ -236,3 +236,27 @@ def test_fused_moe_gate_up_takes_the_gemm_at_prefill_sizes(monkeypatch):
     assert torch.equal(got, moe_gate_up_silu(dx, dw, si, be, nv, K, num_splits=1))
     fused_moe_gate_up(dx[:8], dids[:8], dw)
     assert calls == [1]
+
+
+def test_prefill_path_graph_replay_with_fresh_ids():
+    """fused_moe_gate_up at a prefill size (the two-launch alignment grid, then the
+    expert-block GEMM) captured once and replayed with new routing ids copied into the
+    captured input: every replay equals the eager call on the same ids."""
+    n = 700  # 4200 assignments: the alignment's grid form and 128-row GEMM blocks
+    x, w, ids = _inputs(n, torch.bfloat16, seed=21)
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    fused_moe_gate_up(dx, dids, dw)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fused_moe_gate_up(dx, dids, dw)
+    g = torch.Generator().manual_seed(22)
+    for rep in range(3):
+        new = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(n)])
+        dids.copy_(new.to(DEV))
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fused_moe_gate_up(dx, new.to(DEV), dw)
+        assert torch.equal(out, want), rep
