@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(512, 1)
 k_gate_up_silu_gemm(GemmArgs a) {
   using M = GemmMfma<T>;
   using V8 = typename M::v8;
-  static_assert((BM == 256 && (BNG == 64 || BNG == 128)) || (BM == 128 && BNG == 128), "tile");
+  static_assert((BM == 256 && (BNG == 64 || BNG == 96 || BNG == 128)) || (BM == 128 && BNG == 128), "tile");
   constexpr int TG = BM / 64;                  // token groups of 64
   constexpr int WC = BNG * TG / 8;             // gate (and up) columns per wave
   constexpr int NT = 2 * WC / 16;              // row tiles per wave: NT / 2 gate, NT / 2 up
@@ -154,7 +154,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
 
   // XCD-aware tile order, then GROUP_M token tiles per band of column tiles
   const int mtiles = (a.T + BM - 1) / BM;
-  const int ntiles = a.I / BNG;
+  const int ntiles = (a.I + BNG - 1) / BNG;  // the last one ragged when BNG does not divide I
   int pid = blockIdx.x;
   {
     const int nb = gridDim.x;
@@ -194,7 +194,8 @@ k_gate_up_silu_gemm(GemmArgs a) {
     return X + xrow * a.xs + 8 * c;
   };
   auto w_src = [&](int row, int c) {
-    const int wr = row < BNG ? n0 + row : a.I + n0 + (row - BNG);
+    // columns past I (a ragged last tile) read the last real row and store nothing
+    const int wr = row < BNG ? min(n0 + row, a.I - 1) : a.I + min(n0 + row - BNG, a.I - 1);
     return W + static_cast<int64_t>(wr) * a.ws + 8 * c;
   };
 #pragma unroll
@@ -316,6 +317,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
 #pragma unroll
       for (int t = 0; t < NT / 2; ++t) {
         const int col = n0 + WC * cg + 16 * t + 4 * g;
+        if (col >= a.I) continue;  // a ragged last tile (I a multiple of 16)
         Pack<T, 4> o;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -332,22 +334,27 @@ k_gate_up_silu_gemm(GemmArgs a) {
 
 template <typename T, int BNG, int BM = 256, bool MOE = false>
 int launch_gemm(const GemmArgs& a, hipStream_t st) {
-  const int64_t grid = cdiv(a.T, BM) * (a.I / BNG);
+  const int64_t grid = cdiv(a.T, BM) * cdiv(a.I, BNG);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
   hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, BM, MOE>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
   return launch_status();
 }
 
-// The tile shapes: (tokens, gate columns) of 256 x 64, 256 x 128 or 128 x 128; every one
-// gives each of the 8 waves 64 tokens x (WC gate + WC up) columns.
+// The tile shapes: (tokens, gate columns) of 256 x 64, 256 x 96, 256 x 128 or 128 x 128;
+// every one gives each of the 8 waves 64 tokens x (WC gate + WC up) columns. 96-column
+// tiles need I only a multiple of 16 (the last tile may be ragged), the others I a
+// multiple of the tile.
 template <typename T, bool MOE>
 int launch_tile(const GemmArgs& a, int64_t token_tile, int64_t column_tile, hipStream_t st) {
   if (token_tile == 128) return launch_gemm<T, 128, 128, MOE>(a, st);
+  if (column_tile == 96) return launch_gemm<T, 96, 256, MOE>(a, st);
   return column_tile == 64 ? launch_gemm<T, 64, 256, MOE>(a, st) : launch_gemm<T, 128, 256, MOE>(a, st);
 }
 
-bool gemm_tile_ok(int64_t token_tile, int64_t column_tile) {
-  return (token_tile == 256 && (column_tile == 64 || column_tile == 128)) || (token_tile == 128 && column_tile == 128);
+bool gemm_tile_ok(int64_t token_tile, int64_t column_tile, int64_t inter) {
+  const bool shape = (token_tile == 256 && (column_tile == 64 || column_tile == 96 || column_tile == 128)) ||
+                     (token_tile == 128 && column_tile == 128);
+  return shape && inter >= column_tile && inter % (column_tile == 96 ? 16 : column_tile) == 0;
 }
 
 }  // namespace
@@ -359,8 +366,7 @@ extern "C" int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, cons
   using namespace ember;
   if (tokens == 0) return EMBER_OK;
   if (tokens < 0 || tokens > (int64_t(1) << 24) || hidden < 64 || hidden % 64 != 0 || hidden > (int64_t(1) << 20) ||
-      !gemm_tile_ok(token_tile, column_tile) || inter < column_tile || inter % column_tile != 0 ||
-      inter > (int64_t(1) << 28))
+      !gemm_tile_ok(token_tile, column_tile, inter) || inter > (int64_t(1) << 28))
     return EMBER_EINVAL;
   if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
   if (x == nullptr || w == nullptr || out == nullptr || !aligned16(x) || !aligned16(w) || !aligned16(out))
@@ -385,8 +391,7 @@ extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, 
   if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
   if (num_blocks < 0 || num_valid < 0 || num_tokens < 1 || top_k < 1 || num_experts < 1 || num_blocks > (1 << 22) ||
       num_valid > INT32_MAX / 2 || num_tokens > INT32_MAX || hidden < 64 || hidden % 64 != 0 ||
-      hidden > (int64_t(1) << 20) || !gemm_tile_ok(block_rows, column_tile) || inter < column_tile ||
-      inter % column_tile != 0 || inter > (int64_t(1) << 28))
+      hidden > (int64_t(1) << 20) || !gemm_tile_ok(block_rows, column_tile, inter) || inter > (int64_t(1) << 28))
     return EMBER_EINVAL;
   if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
   if (x == nullptr || w == nullptr || out == nullptr || sorted_ids == nullptr || block_expert == nullptr ||

@@ -44,19 +44,31 @@ MAX_TOKENS = 64           # the kernels' limit
 PACKED_MAX_TOKENS = 64
 FUSED_TOKENS = 16         # default dispatch, row kernel: the kernel up to here, the pair above
 PACKED_FUSED_TOKENS = 32  # default dispatch over a packed weight
-# Prefill sizes (gate_up_silu_gemm): 256 x (64 + 64) tiles while they fit one round of
-# workgroups on the CUs (more workgroups on a short token range), 256 x (128 + 128) beyond
-# (fewer re-reads of x, no second round mostly empty). Measured (bf16, µs, 64 | 128
-# columns): Qwen3-8B 256 tokens (192 | 96 tiles) 69.2 | 94.1; Qwen2.5-7B 256 tokens
-# (296 | 148 tiles) 113.9 | 92.4; Qwen3-8B 1024 tokens 217 | 195.
-GEMM_TILE_SMALL, GEMM_TILE_LARGE = 64, 128
+# Prefill sizes (gate_up_silu_gemm): 256-token tiles of 64, 96 or 128 gate (and as many up)
+# columns. A workgroup's time follows the bytes it streams from L2 into LDS (all 256 x rows
+# plus its 2·columns weight rows, at ~40-45 GB/s per CU), so the call takes about
+# ceil(tiles / CUs) rounds of 256 + 2·columns rows each; gemm_column_tile minimises that.
+# Measured (bf16, µs, 64 | 96 | 128 columns): Qwen3-8B 256 tokens 66.2 | 95.5 | 96.8,
+# 512 tokens 128.0 | 99.0 | 112.6, 8192 tokens 1585 | 1423 | 1324; Qwen2.5-7B 256 tokens
+# 113.7 | 91.2 | 94.0, 512 tokens 167.5 | 164.6 | 179.7, 8192 tokens 2142 | 1961 | 1834.
+GEMM_TILES = (64, 96, 128)
+
+
+def _tile_ok(inter: int, tile: int) -> bool:
+    return inter >= tile and inter % (16 if tile == 96 else tile) == 0
 
 
 def gemm_column_tile(tokens: int, inter: int, device: torch.device) -> int:
-    """The prefill GEMM's column tile from shapes: 64 while the 256-token x 64-column tiles
-    fit one round on the CUs (or 128 does not divide inter), else 128."""
-    tiles = -(-tokens // 256) * (inter // GEMM_TILE_SMALL)
-    return GEMM_TILE_SMALL if tiles <= num_sms(device) or inter % GEMM_TILE_LARGE else GEMM_TILE_LARGE
+    """The prefill GEMM's column tile from shapes: the one of 64, 96 and 128 (96 needs inter
+    only a multiple of 16: its last tile may be ragged) with the fewest rows streamed per
+    CU, ceil(tiles / CUs) x (256 + 2 x columns); the narrower on a tie."""
+    ok = [t for t in GEMM_TILES if _tile_ok(inter, t)]
+    if not ok:
+        raise ValueError(f"gate_up_silu_gemm: no column tile for I {inter}")
+    rows, cus = -(-tokens // 256), max(1, num_sms(device))
+    return min(ok, key=lambda t: (-(-(rows * -(-inter // t)) // cus) * (256 + 2 * t), t))
+
+
 SLAB = 64          # output columns per workgroup
 STEP = 64          # k per pipeline stage
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
@@ -146,8 +158,8 @@ def pack_gate_up_weight(weight: Tensor, num_workgroups: int | None = None) -> Pa
 def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128, token_tile: int = 256) -> Tensor:
     """silu_and_mul(F.linear(x, weight)) as one MFMA GEMM whose epilogue applies the
     activation (`ember_gate_up_silu_gemm`): token_tile x (column_tile gate + column_tile up)
-    tiles ((256, 64), (256, 128) or (128, 128)), any token count. Needs fp16/bf16, H a
-    multiple of 64, I of column_tile."""
+    tiles ((256, 64), (256, 96), (256, 128) or (128, 128)), any token count. Needs fp16/bf16,
+    H a multiple of 64, I of column_tile (of 16 for 96: a ragged last tile)."""
     if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
         raise ValueError(f"gate_up_silu_gemm: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
                          "a [2I, H] gate_up projection")
@@ -159,8 +171,8 @@ def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128, toke
     out = torch.empty((T, I), dtype=x.dtype, device=x.device)
     if T == 0:
         return out.view(*x.shape[:-1], I)
-    if not (_fits(x2, weight, out, max_tokens=1 << 24) and I % column_tile == 0
-            and (token_tile, column_tile) in ((256, 64), (256, 128), (128, 128))):
+    if not (_fits(x2, weight, out, max_tokens=1 << 24) and _tile_ok(I, column_tile)
+            and (token_tile, column_tile) in ((256, 64), (256, 96), (256, 128), (128, 128))):
         raise ValueError(f"gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {I}, "
                          f"column_tile {column_tile}, {x.dtype})")
     _launch("ember_gate_up_silu_gemm", _lib.load().ember_gate_up_silu_gemm, x.device,
@@ -187,7 +199,7 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     if T == 0:
         return out.view(*x.shape[:-1], I)
     limit, default = (PACKED_MAX_TOKENS, PACKED_FUSED_TOKENS) if packed is not None else (MAX_TOKENS, FUSED_TOKENS)
-    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and I % GEMM_TILE_SMALL == 0:
+    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and I % 16 == 0:
         # the fused form asked for at prefill sizes: the MFMA GEMM with the activation epilogue
         return gate_up_silu_gemm(x, weight, column_tile=gemm_column_tile(T, I, x.device))
     if fused is False or (fused is None and T > default) or not _fits(x2, weight, out, limit):

@@ -234,7 +234,7 @@ def test_swiglu_mlp_packed_weights():
 
 
 # ---- prefill sizes: the MFMA GEMM with the activation as its epilogue ----
-@pytest.mark.parametrize("token_tile,tile", [(256, 64), (256, 128), (128, 128)])
+@pytest.mark.parametrize("token_tile,tile", [(256, 64), (256, 96), (256, 128), (128, 128)])
 @pytest.mark.parametrize("tokens", [1, 16, 64, 300])
 def test_gemm_equals_the_packed_kernel(token_tile, tile, tokens):
     """Every accumulator runs over k in order in one chain, as the packed kernel's over
@@ -276,14 +276,18 @@ def test_gemm_rejects_bad_tiles():
 
 
 def test_fused_true_past_64_tokens_runs_the_gemm():
-    """gate_up_silu(..., fused=True) above the decode kernels' limit is the GEMM (64-column
-    tiles while they fit one round on the CUs, else 128); the default keeps the unfused pair."""
-    from emberserve_amd.gate_up_silu import gate_up_silu_gemm
+    """gate_up_silu(..., fused=True) above the decode kernels' limit is the GEMM at the
+    column tile gemm_column_tile picks (its rule is pinned in test_host.py); the default
+    keeps the unfused pair."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gemm_column_tile
     g = torch.Generator().manual_seed(77)
     w = (torch.randn(2 * 256, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    many = 256 * (cus // 4 + 1)  # more 256 x 64 tiles (4 per 256 tokens here) than CUs
-    for tokens, tile in ((100, 64), (600, 64), (many, 128)):
+    tiles = set()
+    for tokens in (100, 600, 256 * (cus // 2 + 1)):
         x = (torch.randn(tokens, 512, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+        tile = gemm_column_tile(tokens, 256, x.device)
+        tiles.add(tile)
         assert torch.equal(gate_up_silu(x, w, fused=True), gate_up_silu_gemm(x, w, column_tile=tile))
         assert torch.equal(gate_up_silu(x, w), gate_up_silu_torch(x, w))
+    assert len(tiles) >= 2

@@ -381,14 +381,20 @@ def test_moe_align_workspace_and_abi_validation():
 
 
 def test_gemm_column_tile_rule(monkeypatch):
-    """64-column tiles while 256-token x 64-column tiles fit one round on the CUs."""
+    """The tile with the fewest rows streamed per CU: ceil(tiles / CUs) x (256 + 2 x cols)."""
     import emberserve_amd.gate_up_silu as gu
     monkeypatch.setattr(gu, "num_sms", lambda device: 256)
     dev = torch.device("cpu")
-    assert gu.gemm_column_tile(256, 12288, dev) == 64      # Qwen3-8B: 192 tiles
-    assert gu.gemm_column_tile(256, 18944, dev) == 128     # Qwen2.5-7B: 296 tiles
-    assert gu.gemm_column_tile(1024, 12288, dev) == 128
-    assert gu.gemm_column_tile(8192, 4864 + 64, dev) == 64  # 128 does not divide inter
+    assert gu.gemm_column_tile(256, 12288, dev) == 64      # Qwen3-8B: 1 round of 192 tiles
+    assert gu.gemm_column_tile(512, 12288, dev) == 96      # 2 x 384 | 1 x 416 | 1 x 512
+    assert gu.gemm_column_tile(8192, 12288, dev) == 128    # 24 x 384 | 16 x 448 | 12 x 512
+    assert gu.gemm_column_tile(256, 18944, dev) == 96      # Qwen2.5-7B: 2 x 384 | 1 x 448
+    assert gu.gemm_column_tile(512, 18944, dev) == 96      # 3 x 384 | 2 x 448 | 2 x 512
+    assert gu.gemm_column_tile(8192, 18944, dev) == 128    # 37 x 384 | 25 x 448 | 19 x 512
+    assert gu.gemm_column_tile(8192, 4864 + 64, dev) == 96  # 128 does not divide inter
+    assert gu.gemm_column_tile(8192, 192, dev) == 64       # 96 tiles of 64 fit one round
+    with pytest.raises(ValueError):
+        gu.gemm_column_tile(256, 40, dev)
 
 
 def test_moe_gate_up_silu_gemm_abi_validation():
