@@ -4,15 +4,16 @@
 //
 // Reference: Qwen2MLP.forward, emberserve/model/qwen2.py:60-61 (gate_up_proj, then
 // ops.silu_and_mul), where the [T, 2I] projection is written and read back. Here it never
-// leaves the chip: each workgroup computes a 256-token x (BNG gate + BNG up) column tile with
-// bf16/fp16 MFMA (v_mfma_f32_16x16x32) and writes only the [256, BNG] activation tile.
+// leaves the chip: each workgroup computes a BM-token x (BNG gate + BNG up) column tile with
+// bf16/fp16 MFMA (v_mfma_f32_16x16x32) and writes only the [BM, BNG] activation tile. Tiles:
+// 256 x 64, 256 x 96 (the last one ragged when 96 does not divide I), 256 x 128, 128 x 128.
 //
 // Structure:
-//   * 8 waves: wave (grp, q) owns tokens 64 q .. 64 q + 63 of the tile and columns
-//     BNG/2 grp .. BNG/2 grp + BNG/2 - 1 of both the gate and the up half, so it holds
-//     (BNG / 16) x 4 accumulator tiles of 16 x 16;
+//   * 8 waves in BM / 64 token groups x 8 / (BM / 64) column groups: each owns 64 tokens of
+//     the tile and WC = BNG BM / 512 columns of both the gate and the up half, so it holds
+//     (2 WC / 16) x 4 accumulator tiles of 16 x 16;
 //   * the tile's operands stream through an LDS ring of "double stages" of 64 k (three for
-//     the 256 x 64 and 128 x 128 tiles; for 256 x 128, where three would not fit, separate
+//     the 256 x 64 and 128 x 128 tiles; for 256 x 96 and 256 x 128, where three would not fit, separate
 //     rings of three weight and two x buffers, 160 KiB: 94 instead of 102 us for Qwen3-8B
 //     at 256 tokens, the same at 8192): rows of 128
 //     bytes (one 64-k line per row), so each direct-to-LDS load (global_load_lds_dwordx4)

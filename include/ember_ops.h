@@ -435,8 +435,8 @@ int ember_moe_gate_up_silu_packed(const void* x, int64_t x_row_stride, int64_t n
  * out [tokens, inter] (out[t, j] = round(round(silu(g)) * u), g and u the dot products
  * rounded to the dtype). x [tokens, hidden], w [2 inter, hidden] (gate rows, then up rows),
  * fp16 or bf16, 16-byte aligned, unit inner stride; hidden a multiple of 64, inter of
- * column_tile. Tiles (token_tile, column_tile): (256, 64), (256, 128) or (128, 128). No
- * workspace. Each accumulator runs over k in order in one chain,
+ * column_tile (of 16 for 96, whose last tile may be ragged). Tiles (token_tile,
+ * column_tile): (256, 64), (256, 96), (256, 128) or (128, 128). No workspace. Each accumulator runs over k in order in one chain,
  * so a token's result equals ember_gate_up_silu_packed's over whole-slab runs bit for bit.
  * Replaces qwen2.py:60-61 (gate_up_proj, then silu_and_mul) without the [T, 2I] round trip. */
 int ember_gate_up_silu_gemm(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int dtype,
