@@ -391,10 +391,11 @@ def _ops(torch, ops, tables):
 
     def gate_up_prefill(cfg, t, hidden, inter, label):
         """The dense MLP's gate_up projection + silu_and_mul at prefill token counts: the
-        MFMA GEMM with the activation as its epilogue (64- and 128-column tiles) beside the
+        MFMA GEMM with the activation as its epilogue (at the column tile gate_up_silu's fused
+        form picks, gemm_column_tile) beside the
         unfused pair (torch linear = hipBLASLt, then silu_and_mul). Bytes: weights + x + the
         [T, I] output; the GEMM is MFMA-bound at these sizes (2·T·2I·H flops)."""
-        from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_torch
+        from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_torch, gemm_column_tile
         wbytes = 2 * inter * hidden * 2
 
         def make(i):
@@ -402,10 +403,10 @@ def _ops(torch, ops, tables):
         nbytes = wbytes + t * hidden * 2 + t * inter * 2
         shape = f"{label}: x[{t},{hidden}] w[{2 * inter},{hidden}] bf16"
         flops = 2 * t * 2 * inter * hidden
-        for tile in (64, 128):
-            out.append(Op("gate_up_silu_gemm", cfg, shape + f" (MFMA GEMM, {tile}+{tile}-column tiles)", nbytes, make,
-                          lambda a, tile=tile: gate_up_silu_gemm(a[0], a[1], column_tile=tile), wbytes + t * hidden * 2,
-                          flops=flops))
+        tile = gemm_column_tile(t, inter, dev)
+        out.append(Op("gate_up_silu_gemm", cfg, shape + f" (MFMA GEMM, {tile}+{tile}-column tiles)", nbytes, make,
+                      lambda a, tile=tile: gate_up_silu_gemm(a[0], a[1], column_tile=tile), wbytes + t * hidden * 2,
+                      flops=flops))
         out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
                       lambda a: gate_up_silu_torch(a[0], a[1]), wbytes + t * hidden * 2, flops=flops))
 
