@@ -199,7 +199,7 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     if T == 0:
         return out.view(*x.shape[:-1], I)
     limit, default = (PACKED_MAX_TOKENS, PACKED_FUSED_TOKENS) if packed is not None else (MAX_TOKENS, FUSED_TOKENS)
-    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and I % 16 == 0:
+    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and any(_tile_ok(I, t) for t in GEMM_TILES):
         # the fused form asked for at prefill sizes: the MFMA GEMM with the activation epilogue
         return gate_up_silu_gemm(x, weight, column_tile=gemm_column_tile(T, I, x.device))
     if fused is False or (fused is None and T > default) or not _fits(x2, weight, out, limit):
