@@ -291,3 +291,7 @@ def test_fused_true_past_64_tokens_runs_the_gemm():
         assert torch.equal(gate_up_silu(x, w, fused=True), gate_up_silu_gemm(x, w, column_tile=tile))
         assert torch.equal(gate_up_silu(x, w), gate_up_silu_torch(x, w))
     assert len(tiles) >= 2
+    # I = 48: no GEMM tile fits, so the fused form falls back to the pair
+    w48 = (torch.randn(2 * 48, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16).to(DEV)
+    x = (torch.randn(100, 512, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    assert torch.equal(gate_up_silu(x, w48, fused=True), gate_up_silu_torch(x, w48))
