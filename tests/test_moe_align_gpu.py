@@ -108,9 +108,11 @@ def test_align_in_a_graph_replays_fresh_ids():
         assert s.cpu().tolist() == want_s and b.cpu().tolist() == want_b, rep
 
 
-@pytest.mark.parametrize("n,e,k", [(512, 64, 6), (513, 64, 6), (1366, 64, 6), (8192, 64, 6), (4096, 256, 8),
-                                   (20000, 1024, 3), (70000, 64, 6)])
-def test_grid_form_matches_one_workgroup_form(n, e, k):
+@pytest.mark.parametrize("n,e,k,dtype", [(512, 64, 6, torch.int64), (513, 64, 6, torch.int64),
+                                         (1366, 64, 6, torch.int64), (1366, 64, 6, torch.int32),
+                                         (8192, 64, 6, torch.int64), (4096, 256, 8, torch.int32),
+                                         (20000, 1024, 3, torch.int64), (70000, 64, 6, torch.int64)])
+def test_grid_form_matches_one_workgroup_form(n, e, k, dtype):
     """Past 3072 assignments the layout comes from a count launch and a placement launch
     over up to 64 workgroups; it equals the one-workgroup form slot for slot and the oracle
     (512 x 6 is the last one-workgroup size at k = 6, 513 x 6 the first grid size; 70000 x 6
@@ -120,8 +122,8 @@ def test_grid_form_matches_one_workgroup_form(n, e, k):
     lib = _lib.load()
     print(f"moe_align grid ids {(n, k)} E={e} workspace {lib.ember_moe_align_workspace_bytes(n * k, e)} B",
           flush=True)
-    s1, b1, _ = moe_align(ids.to(DEV), e, grid=True)
-    s0, b0, _ = moe_align(ids.to(DEV), e, grid=False)
+    s1, b1, _ = moe_align(ids.to(DEV, dtype), e, grid=True)
+    s0, b0, _ = moe_align(ids.to(DEV, dtype), e, grid=False)
     assert torch.equal(s1, s0) and torch.equal(b1, b0)
     if n * k <= 50000:
         want_s, want_b, _ = ref.moe_align(ids, e, 16)
