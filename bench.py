@@ -439,11 +439,12 @@ def _ops(torch, ops, tables):
         out.append(Op("moe_gate_up_silu_packed", cfg, f"moonlight: N={n} top-{k} of {ne} experts ({used} used), "
                       f"w[{ne},{2 * inter},{h}] bf16 packed at load", nbytes, make_packed,
                       lambda a: moe_gate_up_silu(a[0], a[1], sorted_ids, block_expert, nv, k, packed=a[2]), wbytes))
-        if n == 1:  # one token: straight from the routing ids, no alignment
-            from emberserve_amd.moe import moe_gate_up_silu_direct
+        if n <= 12:  # decode batches: straight from the routing ids, no alignment (fused_moe_gate_up's path)
+            from emberserve_amd.moe import moe_direct_half_slabs, moe_gate_up_silu_direct
+            half = moe_direct_half_slabs(n * k, ne, inter, torch.device(dev))
             out.append(Op("moe_gate_up_silu_direct", cfg, f"moonlight: N={n} top-{k} of {ne} experts, from the "
                           "routing ids (no moe_align), packed at load", nbytes, make_packed,
-                          lambda a: moe_gate_up_silu_direct(a[0], ids, a[2]), wbytes))
+                          lambda a: moe_gate_up_silu_direct(a[0], ids, a[2], half_slabs=half), wbytes))
         # the same with the alignment launched each time (ember_moe_align + the grouped kernel)
         out.append(Op("moe_align+gate_up_silu", cfg, f"moonlight: N={n} top-{k} of {ne} experts, align each call",
                       nbytes, make, lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes))

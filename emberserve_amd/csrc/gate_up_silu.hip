@@ -823,6 +823,7 @@ GuPlan gu_plan(int64_t hidden, int64_t inter, int64_t programs) {
 // sums them in k order.
 // Blocks per call: the grid's third dimension (1M assignments in 16-row blocks).
 constexpr int64_t kMoeMaxBlocks = 65535;
+constexpr int kMoeDirectChunks = 4;  // routing ids a direct-mode lane holds: at most 4 x 64 assignments
 
 struct MoeGuArgs {
   const void* x;
@@ -1025,19 +1026,59 @@ k_moe_gate_up_silu_packed(MoeGuArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int n = lane & 15;
   const int g = lane >> 4;
-  // Direct mode: "block" blk is assignment blk alone, in lane 0 (the other 15 lanes are
-  // padding on the same token's row); its expert is read from the routing ids themselves.
+  // Direct mode: "block" blk is assignment blk; its expert is read from the routing ids
+  // themselves. The assignments of one expert form groups of 16 in assignment order (the
+  // order of the aligned layout's runs); the workgroup of each group's first assignment
+  // computes the whole group, one assignment per row n, and the others exit. Each lane holds
+  // up to kMoeDirectChunks x 64 routing ids in registers for the two scans.
   const bool direct = a.topk != nullptr;  // uniform
   int e, id;
   if (direct) {
-    e = a.id_bytes == 8 ? static_cast<int>(static_cast<const int64_t*>(a.topk)[blk])
-                        : static_cast<const int32_t*>(a.topk)[blk];
-    const int64_t e64 = a.id_bytes == 8 ? static_cast<const int64_t*>(a.topk)[blk] : e;
+    auto eid = [&](int i) -> int64_t {
+      return a.id_bytes == 8 ? static_cast<const int64_t*>(a.topk)[i] : static_cast<const int32_t*>(a.topk)[i];
+    };
+    const int64_t e64 = eid(blk);
+    e = static_cast<int>(e64);
     if (e64 < 0 || e64 >= a.E) {  // dropped, as moe_align drops it
       if (threadIdx.x == 0 && tile.slab == 0) atomicOr(a.err, EMBER_ERR_EXPERT_ID);
       return;
     }
-    id = n == 0 ? blk : a.num_valid;
+    const int na = a.num_valid;
+    bool match[kMoeDirectChunks];
+#pragma unroll
+    for (int c = 0; c < kMoeDirectChunks; ++c) {
+      const int i = c * kWave + lane;
+      match[c] = i < na && eid(min(i, na - 1)) == e64;
+    }
+    int before = 0;  // assignments of this expert before blk
+#pragma unroll
+    for (int c = 0; c < kMoeDirectChunks; ++c)
+      before += static_cast<int>(__popcll(__ballot(match[c] && c * kWave + lane < blk)));
+    if (before % 16 != 0) return;  // not the first of its group (uniform)
+    // row n: the (before + n)-th assignment of this expert, padding past the last
+    id = a.num_valid;
+    int seen = 0;
+#pragma unroll
+    for (int c = 0; c < kMoeDirectChunks; ++c) {
+      const uint64_t m = __ballot(match[c]);
+      const int cnt = static_cast<int>(__popcll(m));
+      int k = before + n - seen;
+      if (k >= 0 && k < cnt) {  // the k-th set bit of m
+        uint64_t mm = m;
+        int pos = 0;
+#pragma unroll
+        for (int step = 32; step >= 1; step >>= 1) {
+          const int low = static_cast<int>(__popcll(mm & ((uint64_t(1) << step) - 1)));
+          if (low <= k) {
+            k -= low;
+            mm >>= step;
+            pos += step;
+          }
+        }
+        id = c * kWave + pos;
+      }
+      seen += cnt;
+    }
   } else {
     e = a.block_expert[blk];  // uniform (scalar load)
     if (e < 0 || e >= a.E) return;
@@ -1053,7 +1094,7 @@ k_moe_gate_up_silu_packed(MoeGuArgs a) {
   const T* wp = static_cast<const T*>(a.w) + static_cast<int64_t>(e) * a.wes +
                 (static_cast<int64_t>(tile.split) * nk * slabs + slab) * kUnit + (w * 2 * kWave + lane) * 8;
   const int64_t ustride = static_cast<int64_t>(slabs) * kUnit;
-  int64_t row = direct ? blk / a.a_div : (id >= 0 && id < a.num_valid ? id / a.a_div : 0);
+  int64_t row = id >= 0 && id < a.num_valid ? id / a.a_div : 0;
   if (row >= a.ntok) {
     atomicOr(a.err, EMBER_ERR_ROW_INDEX);
     row = 0;
@@ -1371,7 +1412,7 @@ int ember_moe_gate_up_silu_direct(const void* x, int64_t x_row_stride, int64_t n
                                   int64_t out_row_stride, void* stream) {
   if (num_assignments == 0) return EMBER_OK;
   if (topk_ids == nullptr || (id_bytes != 4 && id_bytes != 8) || (half_slabs != 0 && half_slabs != 1) ||
-      num_assignments < 0 || num_assignments > kMoeMaxBlocks || top_k < 1 || num_assignments % top_k != 0 ||
+      num_assignments < 0 || num_assignments > kMoeDirectChunks * kWave || top_k < 1 || num_assignments % top_k != 0 ||
       num_assignments / top_k > num_tokens)
     return EMBER_EINVAL;
   MoeGuArgs a{};

@@ -114,6 +114,23 @@ def moe_half_slabs(num_valid: int, num_experts: int, inter: int, device: torch.d
     return cus <= busy < 1.5 * cus
 
 
+# fused_moe_gate_up over packed experts: the direct path (no alignment) up to this many
+# tokens. Measured at Moonlight's geometry (µs, align + packed kernel | direct at the
+# moe_direct_half_slabs choice): 1 token 20.3 | 15.5, 2: 26.5 | 21.8, 3: 39.8 | 31.4,
+# 4: 42.3 | 43.1, 8: 74.1 | 65.8, 12: 94.9 | 86.7, 16: 98.8 | 107.5, 32: 115.8 | 120.8.
+DIRECT_MAX_TOKENS = 12
+
+
+def moe_direct_half_slabs(num_assignments: int, num_experts: int, inter: int, device: torch.device) -> bool:
+    """The direct path's workgroup shape: two-wave half-slab workgroups while the four-wave
+    ones over the experts that can be used (min(assignments, experts) x slabs) number from
+    one to five times the CUs. Measured (µs, four-wave | half-slab): 1 token 15.5 | 16.1,
+    2: 31.5 | 28.0 (21.9 | 21.8 on another routing), 3: 33.4 | 31.4, 4: 46.1 | 43.1, 8: 75.4 |
+    65.8, 12: 86.7 | 89.5."""
+    busy, cus = min(num_assignments, num_experts) * max(1, inter // 64), num_sms(device)
+    return cus <= busy < 5 * cus
+
+
 def _workspace_bytes(splits: int, num_valid: int, inter: int, num_blocks: int) -> int:
     return _lib.load().ember_moe_gate_up_silu_workspace_bytes(num_valid, inter, num_blocks, splits)
 
@@ -294,9 +311,10 @@ def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, col
 def moe_gate_up_silu_direct(x: Tensor, topk_ids: Tensor, packed: PackedExperts, *,
                             half_slabs: bool = False) -> Tensor:
     """act [N * k, I] straight from the routing ids, without moe_align
-    (`ember_moe_gate_up_silu_direct`): one workgroup per (assignment, slab). Bit-identical to
-    moe_align + moe_gate_up_silu; meant for one token, whose k experts are distinct (an
-    expert picked by several assignments is read once per assignment)."""
+    (`ember_moe_gate_up_silu_direct`): the assignments of each expert in groups of 16, each
+    group computed by the workgroups of its first assignment (one per slab), the others
+    exiting. Bit-identical to moe_align + moe_gate_up_silu; for decode batches (at most 256
+    assignments)."""
     assert x.dim() == 2 and topk_ids.dim() == 2, (x.shape, topk_ids.shape)
     _require_device("moe_gate_up_silu_direct", x, topk_ids, packed.packed)
     n, k = topk_ids.shape
@@ -320,15 +338,17 @@ def moe_gate_up_silu_direct(x: Tensor, topk_ids: Tensor, packed: PackedExperts, 
 def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_splits: int | None = None,
                       packed: PackedExperts | None = None) -> Tensor:
     """The routed experts' activations [N * k, I] in assignment order (the `act` of
-    moe_triton.py:340): one token over a packed weight straight from the routing ids; from
+    moe_triton.py:340): up to DIRECT_MAX_TOKENS tokens over a packed weight straight from the
+    routing ids; from
     GEMM_FROM assignments the prefill GEMM (`moe_gate_up_silu_gemm`); otherwise moe_align +
     the 16-block kernel (`moe_gate_up_silu`, packed up to PACKED_MAX_ASSIGNMENTS). Every
     path gives the same bits as the 16-block kernel at one k split."""
     aligned = x.is_cuda and fused_enabled(x) and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
     n, k = topk_ids.shape
-    if packed is not None and num_splits is None and n == 1 and aligned:
-        # one token: its k experts are distinct, so no alignment is needed (the same bits)
-        return moe_gate_up_silu_direct(x, topk_ids, packed)
+    if packed is not None and num_splits is None and n <= DIRECT_MAX_TOKENS and aligned:
+        # decode batches: straight from the routing ids, no alignment launch (the same bits)
+        half = moe_direct_half_slabs(n * k, packed.num_experts, packed.inter, x.device)
+        return moe_gate_up_silu_direct(x, topk_ids, packed, half_slabs=half)
     E, two_i, H = w_gate_up.shape
     if (num_splits is None and n * k >= GEMM_FROM and aligned and x.dtype == w_gate_up.dtype
             and x.dtype in SUPPORTED_DTYPES and H % 64 == 0 and (two_i // 2) % 64 == 0

@@ -465,16 +465,18 @@ int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, int64_t num
                                 int64_t out_row_stride, void* stream);
 
 /* The routed experts' gate_up + silu_and_mul over packed weights straight from the routing
- * ids, with no alignment: assignment a = token * top_k + choice (a < num_assignments,
+ * ids, with no alignment: assignment a = token * top_k + choice (a < num_assignments <= 256,
  * topk_ids [num_assignments] int32 or int64 per id_bytes, row-major [tokens, top_k]) gets
  *   out[a, j] = round(round(silu(g)) * u) for expert topk_ids[a], as ember_moe_gate_up_silu
- * computes it, bit for bit. One workgroup per (assignment, slab) reads its expert's rows, so
- * an expert chosen by several assignments is read once per assignment: meant for one token
- * (whose top_k experts are distinct), where it saves the ember_moe_align launch. An expert
- * id outside [0, num_experts) leaves its row unwritten and sets EMBER_ERR_EXPERT_ID.
- * half_slabs as in ember_moe_gate_up_silu_packed. No workspace. No counterpart in the
- * reference's interface: it replaces moe_align + the first grouped GEMM + silu_and_mul
- * (moe_triton.py:332-345) for single-token decode. */
+ * computes it, bit for bit. The grid has a workgroup per (assignment, slab): the
+ * assignments of one expert form groups of 16 in assignment order, the workgroups of each
+ * group's first assignment compute the group (one assignment per tile row) and the others
+ * exit, so each expert's weights are read once per 16 of its assignments. For decode
+ * batches, where it saves the ember_moe_align launch. An expert id outside [0, num_experts)
+ * leaves its row unwritten and sets EMBER_ERR_EXPERT_ID. half_slabs as in
+ * ember_moe_gate_up_silu_packed. No workspace. No counterpart in the reference's interface:
+ * it replaces moe_align + the first grouped GEMM + silu_and_mul (moe_triton.py:332-345) for
+ * decode steps. */
 int ember_moe_gate_up_silu_direct(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed_w,
                                   int dtype, int64_t num_experts, int64_t hidden, int64_t inter, const void* topk_ids,
                                   int id_bytes, int64_t num_assignments, int64_t top_k, int64_t half_slabs, void* out,

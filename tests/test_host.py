@@ -380,6 +380,17 @@ def test_moe_align_workspace_and_abi_validation():
     assert call() == 1  # null pointers
 
 
+def test_moe_direct_half_slab_rule(monkeypatch):
+    """Two-wave half-slab workgroups while min(assignments, experts) x slabs is 1-5x the CUs."""
+    import emberserve_amd.moe as moe
+    monkeypatch.setattr(moe, "num_sms", lambda device: 256)
+    dev = torch.device("cpu")
+    assert not moe.moe_direct_half_slabs(6, 64, 1408, dev)      # 132 workgroups
+    assert moe.moe_direct_half_slabs(12, 64, 1408, dev)         # 264
+    assert moe.moe_direct_half_slabs(48, 64, 1408, dev)         # 1056
+    assert not moe.moe_direct_half_slabs(72, 64, 1408, dev)     # 64 experts: 1408
+
+
 def test_gemm_column_tile_rule(monkeypatch):
     """The tile with the fewest rows streamed per CU: ceil(tiles / CUs) x (256 + 2 x cols)."""
     import emberserve_amd.gate_up_silu as gu

@@ -157,14 +157,12 @@ def test_moe_packed_half_slabs_equal_full_slabs(n):
         moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=2, packed=packed, half_slabs=True)
 
 
-# ---- straight from the routing ids (ember_moe_gate_up_silu_direct) ----
 @pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
-@pytest.mark.parametrize("n", [1, 3])
+@pytest.mark.parametrize("n", [1, 3, 8, 12])
 @pytest.mark.parametrize("half", [False, True])
 def test_moe_direct_equals_the_aligned_path(id_dtype, n, half):
-    """Each assignment alone in lane 0 of its workgroup: the same products in the same order
-    as in its aligned block, so bit-identical (3 tokens: experts picked twice are read twice,
-    still the same bits)."""
+    """Each expert's assignments in groups of 16, computed by the workgroups of each group's
+    first assignment: the same rows and products as its aligned block, so bit-identical."""
     x, w, ids = _inputs(n, torch.bfloat16, seed=400 + n)
     dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
     packed = pack_moe_gate_up_weight(dw)
@@ -172,8 +170,31 @@ def test_moe_direct_equals_the_aligned_path(id_dtype, n, half):
     want = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=1, packed=packed, half_slabs=False)
     got = moe_gate_up_silu_direct(dx, dids.to(id_dtype), packed, half_slabs=half)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
-    if n == 1:  # fused_moe_gate_up takes this path for one token
-        assert torch.equal(fused_moe_gate_up(dx, dids, dw, packed=packed).view(torch.int16), want.view(torch.int16))
+    # fused_moe_gate_up takes this path up to DIRECT_MAX_TOKENS tokens over packed experts
+    assert torch.equal(fused_moe_gate_up(dx, dids, dw, packed=packed).view(torch.int16), want.view(torch.int16))
+
+
+def test_moe_direct_groups_longer_than_16():
+    """40 tokens whose first two choices are experts 0 and 1: runs of 40 assignments, three
+    groups each (16 + 16 + 8), every group's rows in assignment order."""
+    n = 40
+    x, w, ids = _inputs(n, torch.bfloat16, seed=41)
+    ids[:, 0], ids[:, 1] = 0, 1
+    ids[:, 2:] = torch.stack([torch.randperm(E - 2, generator=torch.Generator().manual_seed(t))[:K - 2] + 2
+                              for t in range(n)])
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    packed = pack_moe_gate_up_weight(dw)
+    sorted_ids, block_expert, nv = moe_align(dids, E)
+    want = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, K, num_splits=1, packed=packed, half_slabs=False)
+    for half in (False, True):
+        got = moe_gate_up_silu_direct(dx, dids, packed, half_slabs=half)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), half
+
+
+def test_moe_direct_rejects_more_than_256_assignments():
+    x, w, ids = _inputs(43, torch.bfloat16, seed=43)  # 258 assignments
+    with pytest.raises(RuntimeError):
+        moe_gate_up_silu_direct(x.to(DEV), ids.to(DEV), pack_moe_gate_up_weight(w.to(DEV)))
 
 
 def test_moe_direct_bad_expert_sets_error_bit():
