@@ -111,6 +111,32 @@ def _(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k):
     return _empty((num_valid, w_gate_up.shape[1] // 2), x)
 
 
+@custom_op("emberserve::moe_align", mutates_args=())
+def _moe_align(topk_ids: Tensor, num_experts: int, block_m: int) -> tuple[Tensor, Tensor]:
+    from .moe import moe_align as impl
+    sorted_ids, block_expert, _ = impl(topk_ids, num_experts, block_m)
+    return sorted_ids, block_expert
+
+
+@_moe_align.register_fake
+def _(topk_ids, num_experts, block_m):
+    nv = topk_ids.numel()
+    padded = (nv + num_experts * (block_m - 1) + block_m - 1) // block_m * block_m
+    return (topk_ids.new_empty((padded,), dtype=torch.int32),
+            topk_ids.new_empty((padded // block_m,), dtype=torch.int32))
+
+
+@custom_op("emberserve::fused_moe_gate_up", mutates_args=())
+def _fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor) -> Tensor:
+    from .moe import fused_moe_gate_up as impl
+    return impl(x, topk_ids, w_gate_up)
+
+
+@_fused_moe_gate_up.register_fake
+def _(x, topk_ids, w_gate_up):
+    return _empty((topk_ids.numel(), w_gate_up.shape[1] // 2), x)
+
+
 # ---- embedding (nn.Embedding in model/qwen2.py:172) ---------------------------------------
 
 @custom_op("emberserve::embedding", mutates_args=())
@@ -231,6 +257,15 @@ def gate_up_silu(x: Tensor, weight: Tensor) -> Tensor:
 def moe_gate_up_silu(x: Tensor, w_gate_up: Tensor, sorted_ids: Tensor, block_expert: Tensor, num_valid: int,
                      top_k: int) -> Tensor:
     return torch.ops.emberserve.moe_gate_up_silu(x, w_gate_up, sorted_ids, block_expert, num_valid, top_k)
+
+
+def moe_align(topk_ids: Tensor, num_experts: int, block_m: int = 16) -> tuple[Tensor, Tensor, int]:
+    sorted_ids, block_expert = torch.ops.emberserve.moe_align(topk_ids, num_experts, block_m)
+    return sorted_ids, block_expert, topk_ids.numel()
+
+
+def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor) -> Tensor:
+    return torch.ops.emberserve.fused_moe_gate_up(x, topk_ids, w_gate_up)
 
 
 def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, eps: float, cos: Tensor,

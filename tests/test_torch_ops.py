@@ -59,6 +59,8 @@ def _cases(device: str):
         ("mla_decode", dev(qa[..., :32].contiguous(), qa[..., 32:].contiguous(), lat, bt2, cl2) + (0.3, 32, None)),
         ("gate_up_silu", dev(gx, gw)),
         ("moe_gate_up_silu", dev(gx, mw, sid, bex) + (nv, 2)),
+        ("moe_align", dev(mids) + (4, 16)),
+        ("fused_moe_gate_up", dev(gx, mids, mw)),
     ]
 
 
