@@ -51,12 +51,22 @@
  *                             attn/paged_flash.py:267,276-277
  *   ember_gate_up_silu        silu_and_mul(gate_up_proj(x)) of Qwen2MLP.forward,
  *                             emberserve/model/qwen2.py:60-61 (decode-sized batches)
+ *   ember_gate_up_silu_packed the same over a weight packed at load time
+ *                             (ember_gate_up_silu_pack_weight); up to 64 tokens
+ *   ember_gate_up_silu_gemm   the same at prefill sizes: an MFMA GEMM with the activation
+ *                             in its epilogue
  *   ember_moe_gate_up_silu    the routed experts' grouped gate_up GEMM + silu_and_mul of
  *                             fused_moe_forward, emberserve/model/moe_triton.py:332-345
+ *                             (also _packed, _direct for decode batches, _gemm at prefill)
+ *   ember_moe_align           moe_align, emberserve/model/moe_triton.py:215-254 (one
+ *                             workgroup, or a count + place grid with a workspace)
  *   ember_mla_decode          mla_decode, emberserve/attn/mla_triton.py:119-182 (kernel
  *                             :49-116; fp32 definition attn/mla_torch.py:33-53)
  *   ember_mla_decode_workspace_bytes  its split-K scratch size (the _SCRATCH buffers,
  *                             attn/mla_triton.py:163-166)
+ *   ember_stream_copy         no counterpart: the benchmark's same-size copy ceiling
+ *   ember_paged_decode_noalloc  no counterpart: ember_paged_decode for callers that cannot
+ *                             allocate (a library-owned scratch array)
  */
 #ifndef EMBER_OPS_H
 #define EMBER_OPS_H
