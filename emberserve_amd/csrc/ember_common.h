@@ -33,8 +33,40 @@ __device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v)
 template <typename T>
 __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }  // RNE
 
+// The fp16 cast takes an fp32 value that is already rounded: without the empty asm, hipcc
+// folds `(_Float16)(a * b)` into v_fma_mixlo_f16, which rounds the exact product to fp16
+// once, where the reference rounds it to fp32 first and then to fp16 (the two differ when
+// the fp32 rounding lands on an fp16 tie).
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
+  asm("" : "+v"(v));
+  return static_cast<_Float16>(v);
+}
+
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// Correctly rounded fp32 square root (the value of IEEE sqrt, as torch's CPU rsqrt path
+// 1 / sqrt(x) uses). v_sqrt_f32 alone is accurate to 1 ulp, so its result s is corrected by
+// the sign of the exact residuals x - s' s for the neighbours s' = s -/+ 1 ulp (one fma
+// each): x <= s_dn s puts sqrt(x) at or below the s_dn / s midpoint, x > s_up s above the
+// s / s_up midpoint. Inputs below 2^-96 are scaled by 2^32 first (and the root by 2^-16) so
+// that the neighbours stay normal; zero, infinity, NaN and negative inputs take the
+// hardware result.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const bool tiny = x < 0x1p-96f;
+  const float xs = tiny ? x * 0x1p+32f : x;
+  const float s0 = __builtin_amdgcn_sqrtf(xs);
+  const int bits = __builtin_bit_cast(int, s0);
+  const float s_dn = __builtin_bit_cast(float, bits - 1);
+  const float s_up = __builtin_bit_cast(float, bits + 1);
+  const float r_dn = __builtin_fmaf(-s_dn, s0, xs);
+  const float r_up = __builtin_fmaf(-s_up, s0, xs);
+  float s = r_dn <= 0.f ? s_dn : s0;
+  s = r_up > 0.f ? s_up : s;
+  s = (xs > 0.f && xs < __builtin_huge_valf()) ? s : s0;
+  return tiny ? s * 0x1p-16f : s;
+}
 
 // ---------------------------------------------------------------- 16-byte packs
 
@@ -132,6 +164,62 @@ __device__ __forceinline__ float group_sum(float v) {
     v = lo + hi;
   }
   return v;
+}
+
+// Lane i of a 16-lane DPP row reads lane i + N of the same row (N in 1..15). Lanes whose
+// source lies past the row end read 0; callers only use lanes whose source is in-row.
+template <int N>
+__device__ __forceinline__ float dpp_shl(float v) {
+  static_assert(N >= 1 && N <= 15, "row_shl distance");
+  return dpp_f32<0x100 + N>(v);
+}
+
+// Sum of squares of one row in the order of PyTorch's CPU fp32 sum over a contiguous last
+// dimension (aten/src/ATen/native/cpu/SumKernel.cpp: 8-wide vectors, four interleaved
+// accumulators; for at most 64 vectors per row, i.e. at most 16 vectors per accumulator,
+// every accumulator is a plain left-to-right chain). With that order the kernel's sum is
+// bit-identical to `x.float().pow(2).mean(-1)` * cols on the CPU, so the normalised row
+// rounds exactly as torch-eager's does.
+//
+// Row layout: an aligned group of TPR lanes (TPR in {4, 8, 16}: the group lies inside one
+// DPP row) holds the row's 8-element vectors, vector v in lane v % TPR, register v / TPR,
+// as `sq[v / TPR][e]` = element 8 v + e squared (already rounded to fp32). Accumulator k
+// (k < 4) sums vectors k, k + 4, k + 8, ... element-wise; lane k of the group runs that
+// chain. The four accumulators are then added in order (lane 0 reads lanes 1, 2, 3) and
+// lane 0's eight elements summed left to right; a swizzle hands lane 0's total to the
+// group. Every lane of the group must be active.
+template <int TPR, int NV>
+__device__ __forceinline__ float torch_order_sumsq(const float (&sq)[NV][8]) {
+  constexpr int kVecs = TPR * NV;
+  static_assert(TPR == 4 || TPR == 8 || TPR == 16, "group must fit one DPP row");
+  static_assert(kVecs % 4 == 0 && kVecs <= 64, "sequential-accumulator regime only");
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = sq[0][e];
+#pragma unroll
+  for (int r = 1; r < kVecs / 4; ++r) {
+    const int i = (4 * r) / TPR;  // compile-time after unrolling
+    const int d = (4 * r) % TPR;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = sq[i][e];
+      if (d == 4) x = dpp_shl<4>(x);
+      else if (d == 8) x = dpp_shl<8>(x);
+      else if (d == 12) x = dpp_shl<12>(x);
+      acc[e] = acc[e] + x;
+    }
+  }
+  float tot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float p = acc[e] + dpp_shl<1>(acc[e]);
+    p = p + dpp_shl<2>(acc[e]);
+    p = p + dpp_shl<3>(acc[e]);
+    tot = tot + p;
+  }
+  // ds_swizzle bit mode: lane i reads lane (i & ~(TPR - 1)) of its 32-lane half.
+  constexpr int kAnd = 0x1F & ~(TPR - 1);
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, tot), kAnd));
 }
 
 // ---------------------------------------------------------------- integer division

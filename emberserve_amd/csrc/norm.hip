@@ -14,6 +14,10 @@
 // enough waves to fill the chip.
 #include "ember_common.h"
 
+#ifdef EMBER_NORM_DEBUG_TOTAL
+__device__ float ember_norm_debug_total[4096];
+#endif
+
 namespace ember {
 namespace {
 
@@ -74,7 +78,19 @@ k_rmsnorm(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int64_t 
   }
 
   float total;
-  if constexpr (TPR <= kWave) {
+  if constexpr (VEC == 8 && TPR <= 16 && TPR * NV <= 64) {
+    // Rows of at most 64 packs whose pack count is a multiple of 4 (the launcher caps the
+    // team at 16 lanes for them): PyTorch's CPU summation order, zero packs past the row
+    // end extending the accumulator chains without changing them.
+    (void)ss;
+    float sq[NV][8];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq[i][e] = v[i][e] * v[i][e];
+    }
+    total = nvec % 4 == 0 ? torch_order_sumsq<TPR, NV>(sq) : group_sum<TPR>(ss);
+  } else if constexpr (TPR <= kWave) {
     total = group_sum<TPR>(ss);
   } else {
     __shared__ float partial[kRowsPerBlock][kWavesPerTeam];
@@ -86,8 +102,11 @@ k_rmsnorm(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int64_t 
 #pragma unroll
     for (int k = 0; k < kWavesPerTeam; ++k) total += partial[team][k];
   }
+#ifdef EMBER_NORM_DEBUG_TOTAL
+  if (lane == 0 && live) ember_norm_debug_total[row] = total;
+#endif
   const float var = total / static_cast<float>(cols);
-  const float inv = 1.0f / __fsqrt_rn(var + eps);
+  const float inv = 1.0f / sqrt_rn(var + eps);
 
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -130,7 +149,7 @@ k_rmsnorm_any(const T* __restrict__ x, int64_t xs, const T* __restrict__ r, int6
   float total = 0.f;
 #pragma unroll
   for (int k = 0; k < 256 / kWave; ++k) total += partial[k];
-  const float inv = 1.0f / __fsqrt_rn(total / static_cast<float>(cols) + eps);
+  const float inv = 1.0f / sqrt_rn(total / static_cast<float>(cols) + eps);
   for (int c = threadIdx.x; c < cols; c += 256) {
     float f = to_f32(x[row * xs + c]);
     if constexpr (RESID) f = round_to<T>(f + to_f32(r[row * rs + c]));
@@ -204,7 +223,9 @@ constexpr int64_t kTargetThreads = EMBER_NORM_TARGET_THREADS;
 
 // Picks the row-team width: the narrowest team that holds the row in <= 8 packs per lane,
 // widened (fewer packs per lane) while the launch would have too few threads in flight.
-__host__ inline void pick_team(int64_t nvec, int64_t rows, int* tpr_out, int* nv_out) {
+// Rows of <= 64 packs of 8 elements (a multiple of 4 packs) stay on teams of <= 16 lanes,
+// where the kernel sums the squares in PyTorch's CPU order.
+__host__ inline void pick_team(int64_t nvec, int64_t rows, bool torch_order, int* tpr_out, int* nv_out) {
   int tpr = pow2_ceil(cdiv(nvec, 8));
   if (tpr < 8) tpr = 8;
   if (tpr > 1024) {
@@ -212,7 +233,8 @@ __host__ inline void pick_team(int64_t nvec, int64_t rows, int* tpr_out, int* nv
     return;
   }
   const int64_t p2 = pow2_ceil(nvec);
-  while (tpr < 1024 && tpr * 2 <= p2 && rows * tpr < kTargetThreads) tpr *= 2;
+  const int cap = torch_order && nvec <= 64 && nvec % 4 == 0 ? 16 : 1024;
+  while (tpr < cap && tpr * 2 <= p2 && rows * tpr < kTargetThreads) tpr *= 2;
   *tpr_out = tpr;
   *nv_out = pow2_ceil(cdiv(nvec, tpr));
 }
@@ -225,7 +247,7 @@ int launch_typed(const NormArgs& a) {
   if (RESID) vec_ok = vec_ok && a.rs % VEC == 0 && a.ros % VEC == 0 && aligned16(a.r) && aligned16(a.rout);
   if (vec_ok) {
     int tpr = 0, nv = 0;
-    pick_team(a.cols / VEC, a.rows, &tpr, &nv);
+    pick_team(a.cols / VEC, a.rows, VEC == 8, &tpr, &nv);
     if (tpr != 0) return launch_tpr<T, WT, VEC, RESID>(a, tpr, nv);
   }
   hipLaunchKernelGGL((k_rmsnorm_any<T, RESID>), dim3(static_cast<uint32_t>(a.rows)), dim3(256), 0, a.stream,

@@ -39,6 +39,29 @@ constexpr int kRopeBlock = EMBER_ROPE_BLOCK;  // lanes per workgroup of k_rope a
 namespace ember {
 namespace {
 
+// Sum of squares of one head row held by J lanes as two VEC-element halves per lane (lane j:
+// elements j VEC.. and half + j VEC..). With 8-element packs and J in {4, 8, 16} (head_dim
+// 64, 128, 256 in fp16/bf16) the sum follows PyTorch's CPU order exactly (the first half's
+// packs are vectors 0..J-1, the second half's J..2J-1), so the normalised head matches the
+// reference's rmsnorm bit for bit; otherwise a DPP tree.
+template <int J, int VEC>
+__device__ __forceinline__ float head_sumsq(const float (&f1)[VEC], const float (&f2)[VEC]) {
+  if constexpr (VEC == 8 && (J == 4 || J == 8 || J == 16)) {
+    float sq[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sq[0][e] = f1[e] * f1[e];
+      sq[1][e] = f2[e] * f2[e];
+    }
+    return torch_order_sumsq<J, 2>(sq);
+  } else {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss += f1[e] * f1[e] + f2[e] * f2[e];
+    return group_sum<J>(ss);
+  }
+}
+
 template <typename T, typename WT, int VEC, int J, int G, bool NORM, bool WAVE_TOK>
 __global__ void __launch_bounds__(kRopeBlock)
 k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, int64_t kts, int64_t khs,
@@ -116,11 +139,8 @@ k_rope(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k, i
         f2[e] = to_f32(x2[g].v[e]);
       }
       if constexpr (NORM) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) ss += f1[e] * f1[e] + f2[e] * f2[e];
-        const float tot = group_sum<J>(ss);
-        const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+        const float tot = head_sumsq<J>(f1, f2);
+        const float inv = 1.0f / sqrt_rn(tot / static_cast<float>(2 * half) + eps);
         const bool isq = h < hq;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -199,11 +219,8 @@ k_rope_kv(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ k
       f2[e] = to_f32(x2.v[e]);
     }
     if constexpr (NORM) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) ss += f1[e] * f1[e] + f2[e] * f2[e];
-      const float tot = group_sum<J>(ss);
-      const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+      const float tot = head_sumsq<J>(f1, f2);
+      const float inv = 1.0f / sqrt_rn(tot / static_cast<float>(2 * half) + eps);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         f1[e] = round_to<T>(round_to<T>(f1[e] * inv) * to_f32(wp1.v[e]));
@@ -259,7 +276,7 @@ k_rope_any(T* __restrict__ q, int64_t qts, int64_t qhs, int hq, T* __restrict__ 
       ss += f * f;
     }
     const float tot = group_sum<kWave>(ss);
-    inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(2 * half) + eps);
+    inv = 1.0f / sqrt_rn(tot / static_cast<float>(2 * half) + eps);
   }
   for (int i = lane; i < half; i += kWave) {
     float f1 = to_f32(ptr[i]);
@@ -514,7 +531,7 @@ k_mla(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe, in
         }
       }
       const float tot = group_sum<kWave>(ss);
-      const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+      const float inv = 1.0f / sqrt_rn(tot / static_cast<float>(R) + eps);
       T* lrow = lat == nullptr ? nullptr : lat + toks[u] * lts;
       T* crow = nullptr;
       if constexpr (CACHE) {
@@ -708,7 +725,7 @@ k_mla_tok(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe
     }
   }
   const float tot = group_sum<kWave>(ss);
-  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+  const float inv = 1.0f / sqrt_rn(tot / static_cast<float>(R) + eps);
   T* lrow = lat == nullptr ? nullptr : lat + tok * lts;
   T* crow = nullptr;
   if constexpr (CACHE) {
@@ -759,7 +776,7 @@ k_mla_any(const T* __restrict__ c, int64_t cts, int R, const T* __restrict__ kpe
     ss += f * f;
   }
   const float tot = group_sum<kWave>(ss);
-  const float inv = 1.0f / __fsqrt_rn(tot / static_cast<float>(R) + eps);
+  const float inv = 1.0f / sqrt_rn(tot / static_cast<float>(R) + eps);
   for (int i = lane; i < R; i += kWave)
     lat[tok * lts + i] = from_f32<T>(round_to<T>(to_f32(c[tok * cts + i]) * inv) * to_f32(w[i]));
   const int64_t p = pos[tok];

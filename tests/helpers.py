@@ -4,6 +4,8 @@ from __future__ import annotations
 
 import torch
 
+from tests.sum_order import torch_order_holds
+
 _INT_VIEW = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32}
 
 
@@ -114,3 +116,11 @@ def check_gate_up(got: torch.Tensor, want: torch.Tensor, gu: torch.Tensor, absdo
                              f"u {float(u[t, j])!r} got {float(gotd[t, j])!r} want {float(want[t, j])!r}")
     exact = float((gotd == want.double()).float().mean())
     assert exact >= min_exact, f"{what}: only {exact:.4f} of the elements bit-exact"
+
+
+def norm_bitexact_expected(dtype: torch.dtype, cols: int) -> bool:
+    """The gfx950 norm kernels sum rows of <= 512 half-precision elements (a multiple of 32)
+    in the order of PyTorch's CPU sum, so their normalised rows are bit-identical to the
+    oracle's wherever this host's torch really sums in that order."""
+    return dtype in (torch.float16, torch.bfloat16) and cols % 32 == 0 and cols <= 512 and \
+        torch_order_holds(cols)
