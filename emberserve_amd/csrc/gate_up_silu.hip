@@ -1353,6 +1353,7 @@ int moe_setup(MoeGuArgs& a, const void* x, int64_t x_row_stride, int64_t num_tok
     a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + (part + 255) / 256 * 256);
   }
   a.err = device_error_word();
+  if (a.err == nullptr) return EMBER_ENODEV;
   return EMBER_OK;
 }
 

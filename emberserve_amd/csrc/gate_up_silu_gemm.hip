@@ -119,6 +119,7 @@ struct GemmArgs {
   const int32_t* block_expert;
   int num_valid, top_k, E, ntok;
   int64_t wes;
+  uint32_t* err;  // MOE: EMBER_ERR_ROW_INDEX for a valid assignment whose token is >= ntok
 };
 
 template <typename T, int BNG, int BM, bool MOE>
@@ -188,7 +189,11 @@ k_gate_up_silu_gemm(GemmArgs a) {
     int64_t xrow;
     if (MOE) {  // padding assignments read token 0 and store nothing
       const int id = a.sorted_ids[m0 + xr];
-      xrow = id >= 0 && id < a.num_valid ? min(id / a.top_k, a.ntok - 1) : 0;
+      xrow = id >= 0 && id < a.num_valid ? id / a.top_k : 0;
+      if (xrow >= a.ntok) {  // a corrupt layout: flag it, read token 0 (the row is stored)
+        atomicOr(a.err, EMBER_ERR_ROW_INDEX);
+        xrow = 0;
+      }
     } else {
       xrow = min(m0 + xr, a.T - 1);  // padded tokens: the last real one
     }
@@ -405,7 +410,8 @@ extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, 
   GemmArgs a{x, x_row_stride, w, w_row_stride, out, out_row_stride, static_cast<int>(num_blocks * block_rows),
              static_cast<int>(hidden), static_cast<int>(inter), sorted_ids, block_expert,
              static_cast<int>(num_valid), static_cast<int>(top_k), static_cast<int>(num_experts),
-             static_cast<int>(num_tokens), w_expert_stride};
+             static_cast<int>(num_tokens), w_expert_stride, device_error_word()};
+  if (a.err == nullptr) return EMBER_ENODEV;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16) return launch_tile<_Float16, true>(a, block_rows, column_tile, st);
   return launch_tile<__bf16, true>(a, block_rows, column_tile, st);

@@ -303,7 +303,9 @@ int ember_moe_align(const void* topk_ids, int id_bytes, int64_t num_valid, int64
                     void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace ember;
   if (id_bytes != 4 && id_bytes != 8) return EMBER_EINVAL;
-  if (num_valid < 0 || num_experts < 1 || num_experts > kAlignMaxExperts || block_m < 1 || block_m > 4096)
+  // num_valid <= INT32_MAX / 2 keeps the kernels' int span arithmetic (nv + nseg - 1, ...) in range
+  if (num_valid < 0 || num_valid > INT32_MAX / 2 || num_experts < 1 || num_experts > kAlignMaxExperts ||
+      block_m < 1 || block_m > 4096)
     return EMBER_EINVAL;
   const int64_t need = ember_moe_align_padded_size(num_valid, num_experts, block_m);
   if (need > 0x7fffffffLL || max_padded != need || max_blocks != need / block_m) return EMBER_EINVAL;

@@ -105,6 +105,16 @@ def _fits(x2: Tensor, weight: Tensor, out: Tensor, max_tokens: int = MAX_TOKENS)
             and x2.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0)
 
 
+def _gemm_fits(x2: Tensor, weight: Tensor, out: Tensor) -> bool:
+    """What the prefill GEMM needs beyond its column tile: fp16/bf16, H a multiple of 64,
+    unit inner strides, 16-byte aligned bases (I only has to suit the tile: _tile_ok)."""
+    T, H = x2.shape
+    return (1 <= T <= 1 << 24 and x2.dtype == weight.dtype == out.dtype and x2.dtype in SUPPORTED_DTYPES
+            and H % 64 == 0 and x2.stride(1) == 1 and weight.stride(1) == 1 and out.stride(1) == 1
+            and x2.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0 and out.stride(0) % 4 == 0
+            and x2.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0)
+
+
 class PackedGateUp:
     """A gate_up weight [2I, H] rearranged for `ember_gate_up_silu_packed` run with
     `num_workgroups` workgroups: every MFMA operand fragment of the decode kernel is one
@@ -171,7 +181,7 @@ def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128, toke
     out = torch.empty((T, I), dtype=x.dtype, device=x.device)
     if T == 0:
         return out.view(*x.shape[:-1], I)
-    if not (_fits(x2, weight, out, max_tokens=1 << 24) and _tile_ok(I, column_tile)
+    if not (_gemm_fits(x2, weight, out) and _tile_ok(I, column_tile)
             and (token_tile, column_tile) in ((256, 64), (256, 96), (256, 128), (128, 128))):
         raise ValueError(f"gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {I}, "
                          f"column_tile {column_tile}, {x.dtype})")
@@ -199,7 +209,7 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
     if T == 0:
         return out.view(*x.shape[:-1], I)
     limit, default = (PACKED_MAX_TOKENS, PACKED_FUSED_TOKENS) if packed is not None else (MAX_TOKENS, FUSED_TOKENS)
-    if fused is True and T > limit and _fits(x2, weight, out, 1 << 24) and any(_tile_ok(I, t) for t in GEMM_TILES):
+    if fused is True and T > limit and _gemm_fits(x2, weight, out) and any(_tile_ok(I, t) for t in GEMM_TILES):
         # the fused form asked for at prefill sizes: the MFMA GEMM with the activation epilogue
         return gate_up_silu_gemm(x, weight, column_tile=gemm_column_tile(T, I, x.device))
     if fused is False or (fused is None and T > default) or not _fits(x2, weight, out, limit):

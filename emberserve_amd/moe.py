@@ -119,6 +119,9 @@ def moe_half_slabs(num_valid: int, num_experts: int, inter: int, device: torch.d
 # moe_direct_half_slabs choice): 1 token 20.3 | 15.5, 2: 26.5 | 21.8, 3: 39.8 | 31.4,
 # 4: 42.3 | 43.1, 8: 74.1 | 65.8, 12: 94.9 | 86.7, 16: 98.8 | 107.5, 32: 115.8 | 120.8.
 DIRECT_MAX_TOKENS = 12
+# The direct kernel holds at most this many routing ids (4 per lane of one wave); larger
+# routings (top_k > 21 at 12 tokens) take the aligned path.
+DIRECT_MAX_ASSIGNMENTS = 256
 
 
 def moe_direct_half_slabs(num_assignments: int, num_experts: int, inter: int, device: torch.device) -> bool:
@@ -305,6 +308,8 @@ def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, col
             x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
             _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
             block_expert.numel(), block_rows, num_valid, k, column_tile, out.data_ptr(), out.stride(0))
+    if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
+        raise IndexError("emberserve_amd.moe_gate_up_silu_gemm: assignment id past the token rows")
     return out
 
 
@@ -345,7 +350,8 @@ def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_spl
     path gives the same bits as the 16-block kernel at one k split."""
     aligned = x.is_cuda and fused_enabled(x) and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
     n, k = topk_ids.shape
-    if packed is not None and num_splits is None and n <= DIRECT_MAX_TOKENS and aligned:
+    if (packed is not None and num_splits is None and n <= DIRECT_MAX_TOKENS and n * k <= DIRECT_MAX_ASSIGNMENTS
+            and aligned):
         # decode batches: straight from the routing ids, no alignment launch (the same bits)
         half = moe_direct_half_slabs(n * k, packed.num_experts, packed.inter, x.device)
         return moe_gate_up_silu_direct(x, topk_ids, packed, half_slabs=half)

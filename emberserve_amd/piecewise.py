@@ -1,47 +1,70 @@
-"""Piecewise hipGraph replay of the per-layer ops at padded token buckets: the role of
-emberserve/attn/piecewise_graphs.py (PiecewiseGraphRunner) for this library's kernels.
+"""Segment graphs: hipGraph replay of the row-wise ops between attention calls, at padded
+token buckets (the role emberserve/attn/piecewise_graphs.py plays for the reference's
+model: a prefill or mixed step of any token count replays captured launches for
+everything except attention).
 
-A prefill or mixed step has a variable token count, so one graph per step shape is not
-possible; attention also needs per-step metadata. The pieces around attention are
-row-wise, so they can be captured once per token bucket T and replayed for any step of
-n <= T tokens, with the n real rows at the front of static buffers and T - n padding rows
-behind them (piecewise_graphs.py:12-15). Per layer l and bucket T:
+Design. A decoder stack of L layers, each `pre(l) -> attention(l) -> post(l)`, is cut at
+the attention calls only, which gives L + 1 segments:
 
-    pre graph  [l, T]: pre(l, T)    e.g. add + RMSNorm, qk-norm + rope + paged KV write
-    eager            : attend(l, n) attention on the n real rows, with the step's metadata
-    post graph [l, T]: post(l, T)   e.g. add + RMSNorm, silu_and_mul
+    segment 0      : pre(0)
+    segment l      : post(l - 1), then pre(l)        (1 <= l < L)
+    segment L      : post(L - 1)
 
-The padding rows compute on whatever the static buffers hold and nothing reads their
-results. What they must not do is write shared state: the fused paged-cache writes get
-slot -1 (PAD_SLOT) for every padding row, which the kernels skip (`stage_rows`), so the KV
-cache changes only at the real rows' slots.
+Each segment is one graph per bucket T, so a step replays L + 1 graphs with L eager
+attention calls between them (not 2 L graphs: the post of one layer and the pre of the
+next have no attention between them, so they share a graph). The step's n real rows sit
+at the front of static buffers sized for the largest bucket; rows [n, T) are padding and
+their results are never read (the padded-bucket contract of piecewise_graphs.py:12-15).
+
+Padding rows must not write shared state. The runner owns the step's per-row metadata
+(positions and paged-cache slots, `StepRows`); staging a step fills the padding rows'
+slots with PAD_SLOT (-1), which every cache-writing kernel of this library skips, so the
+KV cache changes at the real rows' slots only.
 
 Every kernel of this library launches on the current stream with no host sync and no
-memset, so the pieces capture as they are. All graphs of one runner share a memory pool
-and one capture stream, and replay one after another on the caller's stream; the split-K
-workspaces of the decode kernels are keyed by that capture stream.
+memset, so a segment captures as it is. All graphs share one memory pool and are captured
+on one stream owned by the runner, largest bucket first (its allocations size the pool;
+smaller buckets then reuse it).
 """
 
 from __future__ import annotations
 
+import bisect
 from typing import Callable
 
 import torch
 
 from .eager import PAD_SLOT
 
-DEFAULT_TOKEN_BUCKETS = (16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192)
+Piece = Callable[[int, int], None]  # (layer, rows) -> None
 
 
-def token_buckets(max_tokens: int, step: int = 0) -> tuple[int, ...]:
-    """Capture buckets, the reference's choice (piecewise_graphs.py:49-60): powers of two
-    from 16 (`step` 0), or powers of two up to `step` and then every `step` tokens up to
-    `max_tokens`."""
-    if step <= 0:
-        return DEFAULT_TOKEN_BUCKETS
-    out = [b for b in DEFAULT_TOKEN_BUCKETS if b <= step]
-    out += list(range(2 * step, max_tokens + 1, step))
+def bucket_ladder(max_tokens: int, linear_step: int = 0, smallest: int = 16) -> tuple[int, ...]:
+    """Token buckets for capture: doubling from `smallest`; with `linear_step` > 0 the
+    doubling stops at `linear_step` and the ladder continues in steps of `linear_step`
+    (finer buckets waste less padded compute at 7B sizes, at the price of more graphs).
+    The ladder ends at the first bucket >= max_tokens."""
+    if max_tokens < 1 or smallest < 1:
+        raise ValueError("bucket_ladder: max_tokens and smallest must be positive")
+    out = []
+    b = smallest
+    cap = linear_step if linear_step > 0 else max_tokens
+    while True:
+        out.append(b)
+        if b >= max_tokens:
+            return tuple(out)
+        if b * 2 > cap:
+            break
+        b *= 2
+    # linear part (linear_step > 0, or a max_tokens between two powers of two)
+    step = linear_step if linear_step > 0 else max_tokens - b
+    while b < max_tokens:
+        b += step
+        out.append(b)
     return tuple(out)
+
+
+DEFAULT_TOKEN_BUCKETS = bucket_ladder(8192)
 
 
 def stage_rows(n: int, bucket: int, positions: torch.Tensor, slots: torch.Tensor,
@@ -58,109 +81,126 @@ def stage_rows(n: int, bucket: int, positions: torch.Tensor, slots: torch.Tensor
         slots[n:bucket].fill_(PAD_SLOT)
 
 
-class _Eager:
-    """A replayable that runs the piece directly (CPU tensors, where there is no graph)."""
+class StepRows:
+    """The per-row metadata of a step, held by the runner at the largest bucket: int64
+    `positions` and `slots`. The pieces read rows [:T] of them."""
 
-    def __init__(self, fn: Callable[[], None]) -> None:
-        self.fn = fn
+    def __init__(self, rows: int, device: torch.device) -> None:
+        self.positions = torch.zeros(rows, dtype=torch.int64, device=device)
+        self.slots = torch.full((rows,), PAD_SLOT, dtype=torch.int64, device=device)
 
-    def replay(self) -> None:
-        self.fn()
+    def stage(self, n: int, bucket: int, positions: torch.Tensor, slots: torch.Tensor) -> None:
+        stage_rows(n, bucket, self.positions, self.slots, positions, slots)
 
 
-class PiecewiseGraphs:
-    """Per-layer pre/post pieces captured at each token bucket.
+class SegmentGraphs:
+    """Graphs of the L + 1 attention-free segments of an L-layer stack, per token bucket.
 
-    pre(layer, t) and post(layer, t) run one layer's pieces on rows [:t] of the caller's
-    static buffers (allocated at the largest bucket). `capture()` warms every piece up on
-    a side stream, then records one graph per (layer, bucket) and piece, largest bucket
-    first. `run(n, attend)` replays the pieces of every layer at the smallest bucket >= n
-    with attend(layer, n) launched eagerly in between; steps above the largest bucket run
-    every piece eagerly at n rows."""
+    `pre(l, t)` / `post(l, t)` run layer l's pieces on rows [:t] of the caller's static
+    buffers (and of `rows.positions` / `rows.slots`). `capture()` records every segment at
+    every bucket. `step(n, attend, positions, slots)` stages the step's metadata, then
+    replays segment 0, attend(0, n), segment 1, ..., attend(L - 1, n), segment L at the
+    smallest bucket >= n and returns that bucket; a step above the largest bucket runs the
+    same sequence eagerly at n rows and returns None. On a CPU device the segments run
+    eagerly (no graphs), which keeps the orchestration testable without a GPU."""
 
-    def __init__(self, num_layers: int, buckets: tuple[int, ...], pre: Callable[[int, int], None],
-                 post: Callable[[int, int], None], device: torch.device | str = "cuda",
-                 max_tokens: int | None = None) -> None:
+    def __init__(self, num_layers: int, buckets, pre: Piece, post: Piece,
+                 device: torch.device | str = "cuda") -> None:
         if num_layers < 1:
-            raise ValueError("PiecewiseGraphs: at least one layer")
-        top = max(buckets) if max_tokens is None else max_tokens
-        bs = sorted({b for b in buckets if 0 < b <= top} | ({max_tokens} if max_tokens else set()))
+            raise ValueError("SegmentGraphs: at least one layer")
+        bs = sorted({int(b) for b in buckets if int(b) > 0})
         if not bs:
-            raise ValueError("PiecewiseGraphs: no bucket")
+            raise ValueError("SegmentGraphs: no bucket")
         self.num_layers = num_layers
-        self.buckets: list[int] = bs
-        self.max_bucket = bs[-1]
+        self.buckets = tuple(bs)
         self.pre, self.post = pre, post
         self.device = torch.device(device)
-        self.graphs_pre: dict[tuple[int, int], object] = {}
-        self.graphs_post: dict[tuple[int, int], object] = {}
+        self.rows = StepRows(bs[-1], self.device)
+        self._graphs: dict[int, list] = {}  # bucket -> one replayable per segment
         self._pool = None
         self._stream = None
-        self._captured = False
 
-    def _record(self, fn: Callable[[], None]):
-        if self.device.type != "cuda":
-            return _Eager(fn)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, pool=self._pool, stream=self._stream):
-            fn()
-        return g
+    # --------------------------------------------------------------------- segments
+    def _segment(self, s: int, t: int) -> None:
+        if s > 0:
+            self.post(s - 1, t)
+        if s < self.num_layers:
+            self.pre(s, t)
 
+    @property
+    def num_segments(self) -> int:
+        return self.num_layers + 1
+
+    @property
+    def captured(self) -> bool:
+        return bool(self._graphs)
+
+    # --------------------------------------------------------------------- capture
     @torch.inference_mode()
-    def capture(self, warmup_iters: int = 1) -> None:
-        if self.device.type == "cuda":
-            self._pool = torch.cuda.graph_pool_handle()
-            self._stream = torch.cuda.Stream(self.device)
-            side = torch.cuda.Stream(self.device)
-            side.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(side):
-                for t in reversed(self.buckets):
-                    for _ in range(warmup_iters):
-                        for i in range(self.num_layers):
-                            self.pre(i, t)
-                            self.post(i, t)
-            torch.cuda.current_stream(self.device).wait_stream(side)
-            torch.cuda.synchronize(self.device)
+    def capture(self, warmup: int = 1) -> None:
+        """Records every (bucket, segment) graph, largest bucket first. Each bucket's
+        segments run `warmup` times eagerly on the capture stream before they are
+        recorded (first-call work such as library handle set-up stays out of the graph)."""
+        if self.device.type != "cuda":
+            for t in self.buckets:
+                self._graphs[t] = [(lambda s=s, t=t: self._segment(s, t)) for s in range(self.num_segments)]
+            return
+        self._pool = torch.cuda.graph_pool_handle()
+        self._stream = torch.cuda.Stream(self.device)
+        self._stream.wait_stream(torch.cuda.current_stream(self.device))
         for t in reversed(self.buckets):
-            for i in range(self.num_layers):
-                self.graphs_pre[i, t] = self._record(lambda i=i, t=t: self.pre(i, t))
-                self.graphs_post[i, t] = self._record(lambda i=i, t=t: self.post(i, t))
-        if self.device.type == "cuda":
-            torch.cuda.synchronize(self.device)
-        self._captured = True
+            with torch.cuda.stream(self._stream):
+                for _ in range(warmup):
+                    for s in range(self.num_segments):
+                        self._segment(s, t)
+            self._stream.synchronize()
+            seg_graphs = []
+            for s in range(self.num_segments):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=self._pool, stream=self._stream):
+                    self._segment(s, t)
+                seg_graphs.append(g.replay)
+            self._graphs[t] = seg_graphs
+        torch.cuda.current_stream(self.device).wait_stream(self._stream)
+        torch.cuda.synchronize(self.device)
 
-    def bucket_for(self, n: int) -> int | None:
-        for b in self.buckets:
-            if b >= n:
-                return b
-        return None
+    # --------------------------------------------------------------------- replay
+    def bucket(self, n: int) -> int | None:
+        """The smallest bucket holding n rows, or None above the largest."""
+        i = bisect.bisect_left(self.buckets, n)
+        return self.buckets[i] if i < len(self.buckets) else None
 
-    def run(self, n: int, attend: Callable[[int, int], None]) -> int | None:
-        """One step of n tokens over every layer; returns the bucket replayed (None: ran
-        eagerly at n rows). The caller has staged the step's rows (`stage_rows`)."""
-        if not self._captured:
-            raise RuntimeError("PiecewiseGraphs.run: call capture() first")
-        t = self.bucket_for(n)
-        for i in range(self.num_layers):
-            if t is None:
-                self.pre(i, n)
-            else:
-                self.graphs_pre[i, t].replay()
-            attend(i, n)
-            if t is None:
-                self.post(i, n)
-            else:
-                self.graphs_post[i, t].replay()
+    def step(self, n: int, attend: Piece, positions: torch.Tensor | None = None,
+             slots: torch.Tensor | None = None) -> int | None:
+        """One step of n tokens through every layer. `positions` / `slots` (n entries each)
+        are staged into `rows` first when given; otherwise the caller staged them."""
+        if not self._graphs:
+            raise RuntimeError("SegmentGraphs.step: call capture() first")
+        t = self.bucket(n)
+        if positions is not None or slots is not None:
+            if positions is None or slots is None:
+                raise ValueError("SegmentGraphs.step: pass positions and slots together")
+            self.rows.stage(n, n if t is None else t, positions, slots)
+        if t is None:
+            for s in range(self.num_segments):
+                self._segment(s, n)
+                if s < self.num_layers:
+                    attend(s, n)
+            return None
+        graphs = self._graphs[t]
+        for s in range(self.num_segments):
+            graphs[s]()
+            if s < self.num_layers:
+                attend(s, n)
         return t
 
     @torch.inference_mode()
     def release(self) -> None:
-        for g in list(self.graphs_pre.values()) + list(self.graphs_post.values()):
-            if hasattr(g, "reset"):
-                g.reset()
-        self.graphs_pre.clear()
-        self.graphs_post.clear()
-        self._captured = False
+        """Drops every graph (and with them the pool's memory)."""
+        self._graphs.clear()
+        self._pool = None
+        self._stream = None
 
     def __repr__(self) -> str:
-        return f"PiecewiseGraphs(buckets={self.buckets}, layers={self.num_layers}, captured={self._captured})"
+        return (f"SegmentGraphs(layers={self.num_layers}, segments={self.num_segments}, "
+                f"buckets={self.buckets}, captured={self.captured})")

@@ -540,7 +540,8 @@ int64_t ember_moe_align_workspace_bytes(int64_t num_valid, int64_t num_experts);
  *     the last run;
  *   block_expert [max_blocks = max_padded / block_m]: the expert of each block, num_experts
  *     past the last used block.
- * max_padded must equal ember_moe_align_padded_size(...). 1 <= num_experts <= 1024. An id
+ * max_padded must equal ember_moe_align_padded_size(...). 1 <= num_experts <= 1024,
+ * 0 <= num_valid <= INT32_MAX / 2. An id
  * outside [0, num_experts) is left out of the layout and sets EMBER_ERR_EXPERT_ID.
  * workspace (may be null) holds the grid form's count table: with at least
  * ember_moe_align_workspace_bytes(...) bytes, a count launch over up to 64 workgroups and a

@@ -267,6 +267,26 @@ def test_gemm_against_oracle(dtype, tokens):
     _check(got[rows][:, cols], x[rows], torch.cat([w[cols], w[12288 + cols]]), f"gemm T={tokens}")
 
 
+@pytest.mark.parametrize("inter", [112, 176, 4880])
+@pytest.mark.parametrize("tokens", [7, 300])
+def test_gemm_ragged_96_column_tile(inter, tokens):
+    """The 96-column tile needs I only a multiple of 16 (and >= 96): its last tile is ragged
+    (I = 112 is one whole tile and 16 columns, 176 one and 80, 4880 fifty and 80).
+    Every column against the oracle, and the default dispatch picks a tile that fits."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gemm_column_tile
+    _say(f"gemm gate_up ragged 96 I={inter} T={tokens}")
+    g = torch.Generator().manual_seed(960 + inter + tokens)
+    x = (torch.randn(tokens, 512, generator=g) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(2 * inter, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16)
+    got = gate_up_silu_gemm(x.to(DEV), w.to(DEV), column_tile=96).cpu()
+    _check(got, x, w, f"gemm 96 I={inter} T={tokens}")
+    if inter % 64 != 0:
+        assert gemm_column_tile(tokens, inter, torch.device(DEV)) == 96
+        fused = gate_up_silu(x.to(DEV), w.to(DEV), fused=True).cpu()
+        if tokens > 64:
+            assert torch.equal(fused, got)
+
+
 def test_gemm_rejects_bad_tiles():
     from emberserve_amd.gate_up_silu import gate_up_silu_gemm
     x = torch.randn(4, 128, device=DEV).to(torch.bfloat16)

@@ -106,6 +106,22 @@ def test_moe_gate_up_bad_assignment_sets_error_bit():
     assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX
 
 
+def test_moe_gemm_bad_assignment_sets_error_bit():
+    """The prefill GEMM through the C ABI with num_tokens 2 while the layout holds the
+    assignments of 4 tokens: rows 2 and 3 read token 0 and flag EMBER_ERR_ROW_INDEX."""
+    from emberserve_amd.ops import _launch
+    x, w, ids = _inputs(4, torch.bfloat16, seed=3)
+    dx, dw = x.to(DEV), w.to(DEV)
+    sorted_ids, block_expert, nv = moe_align(ids.to(DEV), E, 128)
+    out = torch.empty((nv, I), dtype=dx.dtype, device=DEV)
+    _launch("ember_moe_gate_up_silu_gemm", _lib.load().ember_moe_gate_up_silu_gemm, dx.device,
+            dx.data_ptr(), dx.stride(0), 2, dw.data_ptr(), dw.stride(0), dw.stride(1), _lib.dtype_tag(dx.dtype),
+            E, H, I, sorted_ids.data_ptr(), block_expert.data_ptr(), block_expert.numel(), 128, nv, K, 128,
+            out.data_ptr(), out.stride(0))
+    torch.cuda.synchronize()
+    assert _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX
+
+
 # ---- the packed expert layout (ember_moe_gate_up_silu_pack_weight / _packed) ----
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_moe_pack_weight_matches_the_oracle_permutation(dtype):
@@ -195,6 +211,22 @@ def test_moe_direct_rejects_more_than_256_assignments():
     x, w, ids = _inputs(43, torch.bfloat16, seed=43)  # 258 assignments
     with pytest.raises(RuntimeError):
         moe_gate_up_silu_direct(x.to(DEV), ids.to(DEV), pack_moe_gate_up_weight(w.to(DEV)))
+
+
+def test_fused_moe_gate_up_large_top_k_takes_the_aligned_path():
+    """12 tokens at top-24 (288 assignments, past the direct kernel's 256): fused_moe_gate_up
+    over packed experts must fall through to the aligned path rather than raise."""
+    n, k = 12, 24
+    x, w, _ = _inputs(n, torch.bfloat16, seed=44)
+    g = torch.Generator().manual_seed(44)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(n)])
+    dx, dw, dids = x.to(DEV), w.to(DEV), ids.to(DEV)
+    packed = pack_moe_gate_up_weight(dw)
+    sorted_ids, block_expert, nv = moe_align(dids, E)
+    want = moe_gate_up_silu(dx, dw, sorted_ids, block_expert, nv, k, num_splits=1, packed=packed, half_slabs=False)
+    got = fused_moe_gate_up(dx, dids, dw, packed=packed)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    _check(got.cpu(), x, w, ids, "top-24")
 
 
 def test_moe_direct_bad_expert_sets_error_bit():

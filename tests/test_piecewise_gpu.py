@@ -1,5 +1,5 @@
-"""Piecewise graph replay at padded token buckets (emberserve_amd.piecewise; the reference's
-PiecewiseGraphRunner, emberserve/attn/piecewise_graphs.py:12-15, 42, 102-148, 166-184).
+"""Segment-graph replay at padded token buckets (emberserve_amd.piecewise; the role of the
+reference's PiecewiseGraphRunner, emberserve/attn/piecewise_graphs.py:12-15, 166-184).
 
 Two Qwen3-8B-shaped layers (hidden 4096, 32 q + 8 kv heads x 128, intermediate 12288,
 bf16). Pre piece: add + RMSNorm, then qk-norm + rope + paged KV write; post piece: add +
@@ -20,7 +20,7 @@ if not torch.cuda.is_available():
     pytest.skip("needs a GPU", allow_module_level=True)
 
 from emberserve_amd import _lib, ops  # noqa: E402
-from emberserve_amd.piecewise import PiecewiseGraphs, stage_rows  # noqa: E402
+from emberserve_amd.piecewise import SegmentGraphs, stage_rows  # noqa: E402
 from emberserve_amd.rope import RotaryEmbedding  # noqa: E402
 
 DEV = torch.device("cuda")
@@ -82,11 +82,12 @@ def _step_inputs(n: int, g: torch.Generator, table: torch.Tensor):
     return ids, pos, slots, qkv, gu, res
 
 
-def _stage(b: Buffers, n: int, bucket: int, inputs, table) -> None:
+def _stage(b: Buffers, n: int, bucket: int, inputs, table, rows: bool = True) -> None:
     ids, pos, slots, qkv, gu, res = inputs
     b.hidden[:n].copy_(ops.embedding_hip(ids, table))  # the embedding runs outside the graphs
     b.residual[:n].copy_(res)
-    stage_rows(n, bucket, b.positions, b.slots, pos, slots)
+    if rows:
+        stage_rows(n, bucket, b.positions, b.slots, pos, slots)
     for i in range(LAYERS):
         b.qkv[i][:n].copy_(qkv[i])
         b.gate_up[i][:n].copy_(gu[i])
@@ -103,26 +104,27 @@ def test_piecewise_replay_at_padded_buckets_matches_eager():
     gb = Buffers(top, g)
     # the eager side: its own rows, the same weights, its own copy of the caches
     eb = Buffers(top, g, weights=gb.weights, caches=[tuple(c.clone() for c in kv) for kv in gb.caches])
-    runner = PiecewiseGraphs(LAYERS, BUCKETS, lambda i, t: gb.pre(i, t, cos, sin), gb.post, DEV)
-    # warm-up and capture run the pieces on zero rows with slot 0: put the caches back after
+    runner = SegmentGraphs(LAYERS, BUCKETS, lambda i, t: gb.pre(i, t, cos, sin), gb.post, DEV)
+    assert runner.num_segments == LAYERS + 1
+    gb.positions, gb.slots = runner.rows.positions, runner.rows.slots  # the runner owns the step rows
+    # warm-up and capture run the pieces with every slot PAD_SLOT: the caches must not change
     saved = [tuple(c.clone() for c in kv) for kv in gb.caches]
-    gb.slots.fill_(-1)
     runner.capture()
     for (k, v), (k0, v0) in zip(gb.caches, saved):
-        k.copy_(k0)
-        v.copy_(v0)
+        assert torch.equal(k, k0) and torch.equal(v, v0), "capture wrote the KV cache"
     del saved
     assert all(torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) for a, b in zip(gb.caches, eb.caches))
-    for n in (1, 9, 16, 200, 256, 5000):
-        bucket = runner.bucket_for(n)
+    for j, n in enumerate((1, 9, 16, 200, 256, 5000)):
+        bucket = runner.bucket(n)
+        via_step = j % 2 == 1  # odd steps hand the rows to step(), even ones stage them first
         print(f"piecewise step n={n} bucket={bucket}", flush=True)
         inputs = _step_inputs(n, g, table)
         # stale, different padding rows in the graph side's buffers: they must not matter
         for buf in [gb.hidden, gb.residual, *gb.qkv, *gb.gate_up]:
             buf[n:bucket].normal_(generator=g)
-        _stage(gb, n, bucket, inputs, table)
+        _stage(gb, n, bucket, inputs, table, rows=not via_step)
         _stage(eb, n, n, inputs, table)
-        used = runner.run(n, gb.attend)
+        used = runner.step(n, gb.attend, inputs[1], inputs[2]) if via_step else runner.step(n, gb.attend)
         assert used == bucket
         for i in range(LAYERS):  # the same pieces, launched eagerly at the real row count
             eb.pre(i, n, cos, sin)

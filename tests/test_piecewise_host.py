@@ -1,4 +1,4 @@
-"""Host-side checks of the piecewise runner's orchestration (emberserve_amd.piecewise), with
+"""Host-side checks of the piecewise runner's orchestration (emberserve_amd.piecewise.SegmentGraphs), with
 CPU tensors, where the pieces run eagerly instead of from graphs."""
 
 from __future__ import annotations
@@ -8,12 +8,18 @@ import torch
 
 from emberserve_amd import ops
 from emberserve_amd.eager import PAD_SLOT
-from emberserve_amd.piecewise import DEFAULT_TOKEN_BUCKETS, PiecewiseGraphs, stage_rows, token_buckets
+from emberserve_amd.piecewise import DEFAULT_TOKEN_BUCKETS, SegmentGraphs, bucket_ladder, stage_rows
 
 
-def test_token_buckets():
-    assert token_buckets(8192) == DEFAULT_TOKEN_BUCKETS
-    assert token_buckets(1024, 256) == (16, 32, 64, 128, 256, 512, 768, 1024)
+def test_bucket_ladder():
+    assert DEFAULT_TOKEN_BUCKETS == (16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192)
+    assert bucket_ladder(8192) == DEFAULT_TOKEN_BUCKETS
+    assert bucket_ladder(1024, 256) == (16, 32, 64, 128, 256, 512, 768, 1024)
+    assert bucket_ladder(5000) == (16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 5000)
+    assert bucket_ladder(10) == (16,)
+    assert bucket_ladder(1000, 300, smallest=64) == (64, 128, 256, 556, 856, 1156)
+    with pytest.raises(ValueError):
+        bucket_ladder(0)
 
 
 def test_stage_rows_marks_padding():
@@ -26,22 +32,44 @@ def test_stage_rows_marks_padding():
         stage_rows(9, 8, pos, slots, torch.zeros(9, dtype=torch.int64), torch.zeros(9, dtype=torch.int64))
 
 
-def test_run_orders_pieces_and_picks_buckets():
+def test_segments_share_post_and_next_pre():
+    """L layers give L + 1 segments: pre(0) | post(l-1) + pre(l) | post(L-1), with one
+    attention call between consecutive segments, all at the step's bucket."""
     calls = []
-    pw = PiecewiseGraphs(2, (16, 64), lambda i, t: calls.append(("pre", i, t)),
-                         lambda i, t: calls.append(("post", i, t)), device="cpu")
+    sg = SegmentGraphs(3, (64, 16), lambda i, t: calls.append(("pre", i, t)),
+                       lambda i, t: calls.append(("post", i, t)), device="cpu")
+    assert sg.buckets == (16, 64) and sg.num_segments == 4
     with pytest.raises(RuntimeError):
-        pw.run(4, lambda i, n: None)
-    pw.capture()
+        sg.step(4, lambda i, n: None)
+    sg.capture()
+    assert sg.captured
     calls.clear()
-    assert pw.run(5, lambda i, n: calls.append(("attend", i, n))) == 16
-    assert calls == [("pre", 0, 16), ("attend", 0, 5), ("post", 0, 16),
-                     ("pre", 1, 16), ("attend", 1, 5), ("post", 1, 16)]
+    assert sg.step(5, lambda i, n: calls.append(("attend", i, n))) == 16
+    assert calls == [("pre", 0, 16), ("attend", 0, 5), ("post", 0, 16), ("pre", 1, 16), ("attend", 1, 5),
+                     ("post", 1, 16), ("pre", 2, 16), ("attend", 2, 5), ("post", 2, 16)]
     calls.clear()
-    assert pw.run(64, lambda i, n: None) == 64
+    assert sg.step(64, lambda i, n: None) == 64
+    assert {c[2] for c in calls} == {64}
     calls.clear()
-    assert pw.run(65, lambda i, n: None) is None  # above the largest bucket: eager at n rows
-    assert calls == [("pre", 0, 65), ("post", 0, 65), ("pre", 1, 65), ("post", 1, 65)]
+    assert sg.step(65, lambda i, n: calls.append(("attend", i, n))) is None  # eager at n rows
+    assert calls == [("pre", 0, 65), ("attend", 0, 65), ("post", 0, 65), ("pre", 1, 65), ("attend", 1, 65),
+                     ("post", 1, 65), ("pre", 2, 65), ("attend", 2, 65), ("post", 2, 65)]
+    assert sg.bucket(1) == 16 and sg.bucket(17) == 64 and sg.bucket(65) is None
+    sg.release()
+    assert not sg.captured
+
+
+def test_step_stages_the_runner_rows():
+    sg = SegmentGraphs(1, (8,), lambda i, t: None, lambda i, t: None, device="cpu")
+    assert sg.rows.slots.tolist() == [PAD_SLOT] * 8  # nothing is written before a step is staged
+    sg.capture()
+    sg.step(3, lambda i, n: None, torch.tensor([4, 5, 6]), torch.tensor([1, 2, 3]))
+    assert sg.rows.positions.tolist() == [4, 5, 6, 0, 0, 0, 0, 0]
+    assert sg.rows.slots.tolist() == [1, 2, 3] + [PAD_SLOT] * 5
+    with pytest.raises(ValueError):
+        sg.step(3, lambda i, n: None, torch.tensor([4, 5, 6]))
+    with pytest.raises(ValueError):
+        SegmentGraphs(0, (8,), lambda i, t: None, lambda i, t: None, device="cpu")
 
 
 def test_eager_cache_writes_skip_padding_slots():
