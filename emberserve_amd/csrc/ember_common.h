@@ -46,6 +46,14 @@ __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
 
+// The product of two fp16/bf16 values is exact in fp32 (at most 22 significant bits, far
+// from fp32's range limits), so rounding the exact product to T once, as v_fma_mixlo_f16
+// does, equals rounding its fp32 value: the plain cast, free to fold.
+template <typename T>
+__device__ __forceinline__ T half_product(float a_half, float b_half) {
+  return static_cast<T>(a_half * b_half);
+}
+
 // Correctly rounded fp32 square root (the value of IEEE sqrt, as torch's CPU rsqrt path
 // 1 / sqrt(x) uses). v_sqrt_f32 alone is accurate to 1 ulp, so its result s is corrected by
 // the sign of the exact residuals x - s' s for the neighbours s' = s -/+ 1 ulp (one fma

@@ -201,7 +201,7 @@ struct GuRun {
           const float gf = round_to<T>(v[mt][0][i]);
           const float uf = round_to<T>(v[mt][1][i]);
           const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-          o.v[i] = from_f32<T>(act * uf);
+          o.v[i] = half_product<T>(act, uf);
         }
         store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
       }
@@ -912,7 +912,7 @@ __device__ __forceinline__ void moe_finish(const MoeGuArgs& a, f32x4 (&acc)[2], 
       const float gf = round_to<T>(acc[0][i]);
       const float uf = round_to<T>(acc[1][i]);
       const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-      o.v[i] = from_f32<T>(act * uf);
+      o.v[i] = half_product<T>(act, uf);
     }
     store_pack<T, 4>(static_cast<T*>(a.out) + static_cast<int64_t>(id) * a.os + col, o);
   }

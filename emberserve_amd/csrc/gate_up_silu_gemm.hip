@@ -330,7 +330,7 @@ k_gate_up_silu_gemm(GemmArgs a) {
           const float gf = round_to<T>(acc[t][u][r]);
           const float uf = round_to<T>(acc[t + NT / 2][u][r]);
           const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-          o.v[r] = from_f32<T>(act * uf);
+          o.v[r] = half_product<T>(act, uf);
         }
         store_pack<T, 4>(out + static_cast<int64_t>(tok) * a.os + col, o);
       }

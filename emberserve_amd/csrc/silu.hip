@@ -48,7 +48,7 @@ k_silu_mul(const T* __restrict__ x, int64_t xs, T* __restrict__ out, int64_t os,
       for (int e = 0; e < VEC; ++e) {
         const float gf = to_f32(g[k].v[e]);
         const float act = round_to<T>(gf / (1.0f + expf(-gf)));
-        o.v[e] = from_f32<T>(act * to_f32(u[k].v[e]));
+        o.v[e] = half_product<T>(act, to_f32(u[k].v[e]));
       }
       store_stream<T, VEC>(orow + static_cast<int64_t>(vi) * VEC, o);
     }
