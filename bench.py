@@ -396,7 +396,8 @@ def _ops(torch, ops, tables):
         form picks, gemm_column_tile) beside the
         unfused pair (torch linear = hipBLASLt, then silu_and_mul). Bytes: weights + x + the
         [T, I] output; the GEMM is MFMA-bound at these sizes (2·T·2I·H flops)."""
-        from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_torch, gemm_column_tile
+        from emberserve_amd.gate_up_silu import (PACKED_GEMM_TILES, gate_up_silu_gemm, gate_up_silu_gemm_packed,
+                                                 gate_up_silu_torch, gemm_column_tile, pack_gate_up_weight)
         wbytes = 2 * inter * hidden * 2
 
         def make(i):
@@ -410,6 +411,14 @@ def _ops(torch, ops, tables):
                       flops=flops))
         out.append(Op("gate_up_silu_unfused", cfg, shape + " (torch linear + silu_and_mul)", nbytes, make,
                       lambda a: gate_up_silu_torch(a[0], a[1]), wbytes + t * hidden * 2, flops=flops))
+        ptile = gemm_column_tile(t, inter, dev, PACKED_GEMM_TILES)
+
+        def make_packed(i):  # the weight packed once, at load time, outside the timed region
+            x, w = make(i)
+            return x, pack_gate_up_weight(w)
+        out.append(Op("gate_up_silu_gemm_packed", cfg, shape + f" (packed weight, {ptile}+{ptile}-column tiles)",
+                      nbytes, make_packed, lambda a, tile=ptile: gate_up_silu_gemm_packed(a[0], a[1], column_tile=tile),
+                      wbytes + t * hidden * 2, flops=flops))
 
     def moe_gate_up(cfg, n):
         """The routed experts' gate_up + silu_and_mul (moe_triton.py:332-345) at Moonlight's

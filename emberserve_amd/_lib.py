@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libember_ops.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 F32, F16, BF16 = 0, 1, 2
 ERR_EMBED_ID = 1
@@ -75,6 +75,7 @@ SIGNATURES: dict[str, list] = {
     "ember_moe_gate_up_silu_gemm": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
                                     _i64, _i64, _p, _i64, _p],
     "ember_gate_up_silu_packed": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
+    "ember_gate_up_silu_gemm_packed": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
                                _i64, _p, _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],

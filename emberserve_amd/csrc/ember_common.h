@@ -230,6 +230,28 @@ __device__ __forceinline__ float torch_order_sumsq(const float (&sq)[NV][8]) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, tot), kAnd));
 }
 
+// ---------------------------------------------------------------- packed gate_up layout
+//
+// The dense gate_up weight packed for a grid of G decode workgroups: total = (I / 64) (H / 64)
+// units of 16 KiB, unit u = slab * (H / 64) + j holding the 64-row slab's gate and up rows
+// over k in [64 j, 64 j + 64) as MFMA operand fragments. The decode kernel's workgroups own
+// contiguous unit runs; the prefill GEMM reads the same array by unit.
+// Workgroup b's units are [start(b), start(b + 1)), start(b) = floor(b total / G); the
+// workgroup that holds unit u is floor(((u + 1) G - 1) / total).
+__device__ __host__ __forceinline__ int64_t gu_start(int64_t b, int64_t total, int64_t G) { return b * total / G; }
+__device__ __host__ __forceinline__ int64_t gu_owner(int64_t u, int64_t total, int64_t G) {
+  return ((u + 1) * G - 1) / total;
+}
+// Where the packed weight layout keeps unit t of workgroup b's run, in units: runs hold q =
+// total / G or q + 1 units, so the t-th units of all workgroups (t < q) are stored side by
+// side in workgroup order, t-major, and the extra units of the longer runs follow, also in
+// workgroup order. At any moment the grid then reads one narrow window of the array.
+__device__ __host__ __forceinline__ int64_t gu_packed_pos(int64_t b, int64_t t, int64_t total, int64_t G) {
+  const int64_t q = total / G;
+  return t < q ? t * G + b : q * G + (gu_start(b, total, G) - b * q);
+}
+
+
 // ---------------------------------------------------------------- integer division
 
 // Division of a uint32 n < 2^31 by a runtime-constant d >= 1 with one mul-hi

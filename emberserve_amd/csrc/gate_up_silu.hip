@@ -130,21 +130,6 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup b's units are [start(b), start(b + 1)), start(b) = floor(b total / G); the
-// workgroup that holds unit u is floor(((u + 1) G - 1) / total).
-__device__ __host__ __forceinline__ int64_t gu_start(int64_t b, int64_t total, int64_t G) { return b * total / G; }
-__device__ __host__ __forceinline__ int64_t gu_owner(int64_t u, int64_t total, int64_t G) {
-  return ((u + 1) * G - 1) / total;
-}
-// Where the packed weight layout keeps unit t of workgroup b's run, in units: runs hold q =
-// total / G or q + 1 units, so the t-th units of all workgroups (t < q) are stored side by
-// side in workgroup order, t-major, and the extra units of the longer runs follow, also in
-// workgroup order. At any moment the grid then reads one narrow window of the array.
-__device__ __host__ __forceinline__ int64_t gu_packed_pos(int64_t b, int64_t t, int64_t total, int64_t G) {
-  const int64_t q = total / G;
-  return t < q ? t * G + b : q * G + (gu_start(b, total, G) - b * q);
-}
-
 // A workgroup barrier that waits for this wave's LDS reads but not for its global loads
 // (__syncthreads() carries a workgroup fence, which waits for every outstanding load and
 // would drain the load ring each step). The asm clobbers keep the compiler from moving

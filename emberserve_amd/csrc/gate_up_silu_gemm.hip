@@ -120,11 +120,49 @@ struct GemmArgs {
   int num_valid, top_k, E, ntok;
   int64_t wes;
   uint32_t* err;  // MOE: EMBER_ERR_ROW_INDEX for a valid assignment whose token is >= ntok
+  // packed weights (PK kernels only): w is the decode kernels' packed array for a grid of
+  // pk_G workgroups over pk_total units (pk_total = (I / 64) (H / 64))
+  int64_t pk_total, pk_G;
 };
 
-template <typename T, int BNG, int BM, bool MOE>
+// Walks the packed units of one 64-row slab, u = slab * nk + j for j = 0, 1, ...: the unit's
+// place in the packed array, tracking its owner workgroup b and b's run [start, next)
+// incrementally (a division only where the walk crosses into the next run).
+struct PackedSlabWalk {
+  int64_t u, last, b, start, next, q, total, G;
+  __device__ void init(int64_t slab, int64_t nk, int64_t total_, int64_t G_) {
+    total = total_;
+    G = G_;
+    q = total / G;
+    u = slab * nk;
+    last = u + nk - 1;
+    b = gu_owner(u, total, G);
+    start = gu_start(b, total, G);
+    next = gu_start(b + 1, total, G);
+  }
+  // the unit's element offset (16 KiB units)
+  template <typename T>
+  __device__ int64_t elem_offset() const {
+    const int64_t t = u - start;
+    const int64_t pos = t < q ? t * G + b : q * G + (start - b * q);
+    return pos * (16384 / static_cast<int64_t>(sizeof(T)));
+  }
+  __device__ void advance() {  // past the slab's last unit it stays there
+    if (u == last) return;
+    ++u;
+    if (u >= next) {
+      ++b;
+      start = next;
+      next = gu_start(b + 1, total, G);
+    }
+  }
+};
+
+template <typename T, int BNG, int BM, bool MOE, bool PK = false>
 __global__ void __launch_bounds__(512, 1)
 k_gate_up_silu_gemm(GemmArgs a) {
+  static_assert(!(MOE && PK), "packed weights are dense only");
+  static_assert(!PK || BNG % 64 == 0, "packed tiles are whole 64-row slabs");
   using M = GemmMfma<T>;
   using V8 = typename M::v8;
   static_assert((BM == 256 && (BNG == 64 || BNG == 96 || BNG == 128)) || (BM == 128 && BNG == 128), "tile");
@@ -204,35 +242,64 @@ k_gate_up_silu_gemm(GemmArgs a) {
     const int wr = row < BNG ? min(n0 + row, a.I - 1) : a.I + min(n0 + row - BNG, a.I - 1);
     return W + static_cast<int64_t>(wr) * a.ws + 8 * c;
   };
+  // Packed weights: the tile's weight region is its S slabs' 16 KiB units side by side, in
+  // the units' own fragment order (1 KiB block ins of slab ins / 16 is bytes
+  // [1024 (ins % 16), +1024) of the slab's unit), so every load is 1 KiB of contiguous
+  // memory and the fragment reads need no swizzle.
+  constexpr int S = PK ? BNG / 64 : 1;
+  bool isw[LOADS];  // a weight load (uniform)
+  int wsl[LOADS];   // PK: the slab of a weight load
+  auto pk_src = [&](int ins) { return W + (ins % 16) * 512 + 8 * lane; };
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     if (SPLIT) {  // block offsets within the operand's own buffer
       const int ins = i < WL ? WL * w + i : (LOADS - WL) * w + (i - WL);
       const int row = 8 * ins + (lane >> 3);
       const int c = (lane & 7) ^ (row & 7);
-      src[i] = i < WL ? w_src(row, c) : x_src(row, c);
+      isw[i] = i < WL;
+      wsl[i] = ins / 16;
+      src[i] = i < WL ? (PK ? pk_src(ins) : w_src(row, c)) : x_src(row, c);
       dst[i] = ins * 1024;
     } else {
       const int ins = LOADS * w + i;  // 0 .. 2 BNG / 8 + BM / 8 - 1
       const int row = 8 * ins + (lane >> 3);
       const int c = (lane & 7) ^ (row & 7);
-      src[i] = row < 2 * BNG ? w_src(row, c) : x_src(row - 2 * BNG, c);
+      isw[i] = row < 2 * BNG;  // whole blocks: uniform
+      wsl[i] = ins / 16;
+      src[i] = isw[i] ? (PK ? pk_src(ins) : w_src(row, c)) : x_src(row - 2 * BNG, c);
       dst[i] = ins * 1024;  // the weight region is rows 0 .. 2 BNG - 1, the x region follows
     }
   }
   const int nd = a.H / 64;  // double stages
+  PackedSlabWalk walk[S];
+  if (PK) {
+#pragma unroll
+    for (int ss = 0; ss < S; ++ss) walk[ss].init(n0 / 64 + ss, nd, a.pk_total, a.pk_G);
+  }
+  // element offsets of this double stage's weight units (PK); the walks then move on
+  int64_t wofs[S];
+  auto next_units = [&]() {
+#pragma unroll
+    for (int ss = 0; ss < S; ++ss) {
+      wofs[ss] = walk[ss].template elem_offset<T>();
+      walk[ss].advance();
+    }
+  };
+  auto wk = [&](int i, int kk) -> int64_t { return PK ? wofs[wsl[i]] : kk; };
   auto wbuf = [&](int d) { return lds + (SPLIT ? (d % 3) * WREG : (d % NBUF) * DST); };
   auto xbuf = [&](int d) { return lds + (SPLIT ? 3 * WREG + (d % 2) * XREG : (d % NBUF) * DST + WREG); };
   auto issue = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
+    if (PK) next_units();
     unsigned char* st = lds + (d % NBUF) * DST;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) gemm_load_lds16(src[i] + kk, st + dst[i]);
+    for (int i = 0; i < LOADS; ++i) gemm_load_lds16(src[i] + (isw[i] ? wk(i, kk) : kk), st + dst[i]);
   };
   auto issue_w = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
+    if (PK) next_units();
 #pragma unroll
-    for (int i = 0; i < WL; ++i) gemm_load_lds16(src[i] + kk, wbuf(d) + dst[i]);
+    for (int i = 0; i < WL; ++i) gemm_load_lds16(src[i] + wk(i, kk), wbuf(d) + dst[i]);
   };
   auto issue_x = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
@@ -241,8 +308,14 @@ k_gate_up_silu_gemm(GemmArgs a) {
   };
   int woff[NT], xoff[4];
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
-    woff[t] = ((t < NT / 2 ? 0 : BNG) + WC * cg + 16 * (t % (NT / 2)) + n) * kGemmRowB;
+  for (int t = 0; t < NT; ++t) {
+    if (PK) {  // slab c / 64, fragment (row tile (c % 64) / 16, part) of the unit's first k32 half
+      const int c = WC * cg + 16 * (t % (NT / 2));
+      woff[t] = (c / 64) * 16384 + (((c % 64) / 16) * 2 + (t < NT / 2 ? 0 : 1)) * 1024 + 16 * lane;
+    } else {
+      woff[t] = ((t < NT / 2 ? 0 : BNG) + WC * cg + 16 * (t % (NT / 2)) + n) * kGemmRowB;
+    }
+  }
 #pragma unroll
   for (int u = 0; u < 4; ++u) xoff[u] = (64 * q + 16 * u + n) * kGemmRowB;
   const int sw = n & 7;  // row % 8 of every fragment row
@@ -283,7 +356,8 @@ k_gate_up_silu_gemm(GemmArgs a) {
     const unsigned char* sx_ = xbuf(j);
     const int co = ((4 * (s & 1) + g) ^ sw) << 4;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) fw[t] = *reinterpret_cast<const V8*>(sw_ + woff[t] + co);
+    for (int t = 0; t < NT; ++t)
+      fw[t] = *reinterpret_cast<const V8*>(sw_ + woff[t] + (PK ? (s & 1) * 8192 : co));
 #pragma unroll
     for (int u = 0; u < 4; ++u) fx[u] = *reinterpret_cast<const V8*>(sx_ + xoff[u] + co);
     if (!even) gemm_wait_vm<kNextLanded>();  // the next double stage has landed
@@ -338,11 +412,12 @@ k_gate_up_silu_gemm(GemmArgs a) {
   }
 }
 
-template <typename T, int BNG, int BM = 256, bool MOE = false>
+template <typename T, int BNG, int BM = 256, bool MOE = false, bool PK = false>
 int launch_gemm(const GemmArgs& a, hipStream_t st) {
   const int64_t grid = cdiv(a.T, BM) * cdiv(a.I, BNG);
   if (grid > 0x7fffffffLL) return EMBER_EINVAL;
-  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, BM, MOE>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st, a);
+  hipLaunchKernelGGL((k_gate_up_silu_gemm<T, BNG, BM, MOE, PK>), dim3(static_cast<uint32_t>(grid)), dim3(512), 0, st,
+                     a);
   return launch_status();
 }
 
@@ -415,4 +490,36 @@ extern "C" int ember_moe_gate_up_silu_gemm(const void* x, int64_t x_row_stride, 
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == EMBER_F16) return launch_tile<_Float16, true>(a, block_rows, column_tile, st);
   return launch_tile<__bf16, true>(a, block_rows, column_tile, st);
+}
+
+extern "C" int ember_gate_up_silu_gemm_packed(const void* x, int64_t x_row_stride, const void* packed, int dtype,
+                                              int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups,
+                                              int64_t token_tile, int64_t column_tile, void* out,
+                                              int64_t out_row_stride, void* stream) {
+  using namespace ember;
+  if (tokens == 0) return EMBER_OK;
+  if (tokens < 0 || tokens > (int64_t(1) << 24) || hidden < 64 || hidden % 64 != 0 || hidden > (int64_t(1) << 20) ||
+      inter < 64 || inter % 64 != 0 || inter > (int64_t(1) << 28) || num_workgroups < 1)
+    return EMBER_EINVAL;
+  const bool shape = (token_tile == 256 && (column_tile == 64 || column_tile == 128)) ||
+                     (token_tile == 128 && column_tile == 128);
+  if (!shape || inter % column_tile != 0) return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || packed == nullptr || out == nullptr || !aligned16(x) || !aligned16(packed) || !aligned16(out))
+    return EMBER_EINVAL;
+  if (x_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 || out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  const int64_t total = (inter / 64) * (hidden / 64);
+  GemmArgs a{x, x_row_stride, packed, 0, out, out_row_stride, static_cast<int>(tokens),
+             static_cast<int>(hidden), static_cast<int>(inter), nullptr, nullptr, 0, 1, 0, 0, 0, nullptr,
+             total, num_workgroups < total ? num_workgroups : total};  // the packing's grid
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16) {
+    if (token_tile == 128) return launch_gemm<_Float16, 128, 128, false, true>(a, st);
+    return column_tile == 64 ? launch_gemm<_Float16, 64, 256, false, true>(a, st)
+                             : launch_gemm<_Float16, 128, 256, false, true>(a, st);
+  }
+  if (token_tile == 128) return launch_gemm<__bf16, 128, 128, false, true>(a, st);
+  return column_tile == 64 ? launch_gemm<__bf16, 64, 256, false, true>(a, st)
+                           : launch_gemm<__bf16, 128, 256, false, true>(a, st);
 }

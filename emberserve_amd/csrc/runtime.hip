@@ -45,7 +45,7 @@ __host__ int device_cu_count() {
 
 extern "C" {
 
-int ember_abi_version(void) { return 15; }
+int ember_abi_version(void) { return 16; }
 
 const char* ember_status_string(int status) {
   switch (status) {

@@ -58,11 +58,11 @@ def _tile_ok(inter: int, tile: int) -> bool:
     return inter >= tile and inter % (16 if tile == 96 else tile) == 0
 
 
-def gemm_column_tile(tokens: int, inter: int, device: torch.device) -> int:
-    """The prefill GEMM's column tile from shapes: the one of 64, 96 and 128 (96 needs inter
-    only a multiple of 16: its last tile may be ragged) with the fewest rows streamed per
-    CU, ceil(tiles / CUs) x (256 + 2 x columns); the narrower on a tie."""
-    ok = [t for t in GEMM_TILES if _tile_ok(inter, t)]
+def gemm_column_tile(tokens: int, inter: int, device: torch.device, tiles: tuple[int, ...] = GEMM_TILES) -> int:
+    """The prefill GEMM's column tile from shapes: the one of `tiles` (64, 96 and 128; 96
+    needs inter only a multiple of 16: its last tile may be ragged) with the fewest rows
+    streamed per CU, ceil(tiles / CUs) x (256 + 2 x columns); the narrower on a tie."""
+    ok = [t for t in tiles if _tile_ok(inter, t)]
     if not ok:
         raise ValueError(f"gate_up_silu_gemm: no column tile for I {inter}")
     rows, cus = -(-tokens // 256), max(1, num_sms(device))
@@ -191,10 +191,91 @@ def gate_up_silu_gemm(x: Tensor, weight: Tensor, *, column_tile: int = 128, toke
     return out.view(*x.shape[:-1], I)
 
 
-def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None,
+PACKED_GEMM_TILES = (64, 128)  # the packed GEMM's column tiles: whole 64-row slabs
+
+
+def gate_up_silu_gemm_packed(x: Tensor, packed: PackedGateUp, *, column_tile: int | None = None,
+                             token_tile: int = 256) -> Tensor:
+    """gate_up_silu_gemm over the packed weight (`ember_gate_up_silu_gemm_packed`): the same
+    tiles but the 96-column one, the same results bit for bit. With it the packed copy is
+    the only gate_up weight a model needs (decode kernels and prefill read it)."""
+    H, I = packed.hidden, packed.inter
+    if x.shape[-1] != H or x.dtype != packed.dtype:
+        raise ValueError(f"gate_up_silu_gemm_packed: x {tuple(x.shape)} {x.dtype} does not match the packed "
+                         f"[{2 * I}, {H}] {packed.dtype} weight")
+    _require_device("gate_up_silu_gemm_packed", x, packed.packed)
+    x2 = x.reshape(-1, H)
+    T = x2.shape[0]
+    out = torch.empty((T, I), dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out.view(*x.shape[:-1], I)
+    if column_tile is None:
+        column_tile = gemm_column_tile(T, I, x.device, PACKED_GEMM_TILES)
+    if not (T <= 1 << 24 and x2.stride(1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0
+            and (token_tile, column_tile) in ((256, 64), (256, 128), (128, 128)) and I % column_tile == 0):
+        raise ValueError(f"gate_up_silu_gemm_packed: shape, stride or tile not supported (I {I}, "
+                         f"column_tile {column_tile}, token_tile {token_tile})")
+    _launch("ember_gate_up_silu_gemm_packed", _lib.load().ember_gate_up_silu_gemm_packed, x.device,
+            x2.data_ptr(), x2.stride(0), packed.packed.data_ptr(), _lib.dtype_tag(x.dtype), T, H, I,
+            packed.num_workgroups, token_tile, column_tile, out.data_ptr(), out.stride(0))
+    return out.view(*x.shape[:-1], I)
+
+
+def gate_up_silu(x: Tensor, weight: Tensor | None, *, num_workgroups: int | None = None,
                  fused: bool | None = None, packed: PackedGateUp | None = None) -> Tensor:
     """silu_and_mul(F.linear(x, weight)) with weight [2I, H] (qwen2.py:60-61). With `packed`
-    (`pack_gate_up_weight(weight)`), the fused kernel reads the packed copy instead."""
+    (`pack_gate_up_weight(weight)`), the fused kernel reads the packed copy instead. With
+    `packed` and weight None (a model that dropped the unpacked weight) every size runs on
+    the packed copy: the decode kernel up to PACKED_MAX_TOKENS tokens, the packed prefill
+    GEMM above."""
+    if weight is None:
+        if packed is None:
+            raise ValueError("gate_up_silu: weight None needs the packed weight")
+        if fused is False:
+            raise ValueError("gate_up_silu: the unfused pair needs the unpacked weight")
+        if x.reshape(-1, packed.hidden).shape[0] > PACKED_MAX_TOKENS:
+            return gate_up_silu_gemm_packed(x, packed)
+        return _packed_decode(x, packed, num_workgroups)
+    return _gate_up_silu_decode(x, weight, num_workgroups, fused, packed)
+
+
+def _packed_decode(x: Tensor, packed: PackedGateUp, num_workgroups: int | None) -> Tensor:
+    """The decode kernel over the packed weight alone, 1..PACKED_MAX_TOKENS tokens."""
+    H, I = packed.hidden, packed.inter
+    if x.shape[-1] != H or x.dtype != packed.dtype:
+        raise ValueError(f"gate_up_silu: x {tuple(x.shape)} {x.dtype} does not match the packed "
+                         f"[{2 * I}, {H}] {packed.dtype} weight")
+    _require_device("gate_up_silu", x, packed.packed)
+    if num_workgroups is not None and int(num_workgroups) != packed.num_workgroups:
+        raise ValueError(f"gate_up_silu: the weight was packed for {packed.num_workgroups} workgroups, "
+                         f"not {num_workgroups}")
+    x2 = x.reshape(-1, H)
+    T = x2.shape[0]
+    out = torch.empty((T, I), dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out.view(*x.shape[:-1], I)
+    if not (x2.stride(1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0):
+        raise ValueError("gate_up_silu: x needs unit inner stride, rows a multiple of 8 elements apart "
+                         "and 16-byte alignment for the packed weight")
+    _launch_packed(x2, packed, packed.num_workgroups, out)
+    return out.view(*x.shape[:-1], I)
+
+
+def _launch_packed(x2: Tensor, packed: PackedGateUp, programs: int, out: Tensor) -> None:
+    T, H = x2.shape
+    I = packed.inter
+    tiles = -(-T // 16)
+    ws = _SCRATCH.get((programs, tiles, H, I), lambda: _workspace_bytes(programs, tiles, H, I), x2.device)
+    _launch("ember_gate_up_silu_packed", _lib.load().ember_gate_up_silu_packed, x2.device,
+            x2.data_ptr(), x2.stride(0), packed.packed.data_ptr(), _lib.dtype_tag(x2.dtype),
+            T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+    if _check_indices():
+        need, slabs = _workspace_bytes(programs, tiles, H, I), I // SLAB
+        _SCRATCH.verify_counters(ws, need - round_up(slabs * 4, 256), need - round_up(slabs * 4, 256) + slabs * 4)
+
+
+def _gate_up_silu_decode(x: Tensor, weight: Tensor, num_workgroups: int | None, fused: bool | None,
+                         packed: PackedGateUp | None) -> Tensor:
     if weight.dim() != 2 or weight.shape[0] % 2 != 0 or x.shape[-1] != weight.shape[1]:
         raise ValueError(f"gate_up_silu: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match "
                          "a [2I, H] gate_up projection")
@@ -222,18 +303,16 @@ def gate_up_silu(x: Tensor, weight: Tensor, *, num_workgroups: int | None = None
         programs = packed.num_workgroups
     if programs < 1:
         raise ValueError(f"gate_up_silu: num_workgroups must be >= 1, got {programs}")
-    tiles = -(-T // 16)
-    ws = _SCRATCH.get((programs, tiles, H, I), lambda: _workspace_bytes(programs, tiles, H, I), x.device)
     if packed is not None:
         if (packed.hidden, packed.inter, packed.dtype, packed.device) != (H, I, x.dtype, x.device):
             raise ValueError("gate_up_silu: the packed weight does not match x and weight")
-        _launch("ember_gate_up_silu_packed", _lib.load().ember_gate_up_silu_packed, x.device,
-                x2.data_ptr(), x2.stride(0), packed.packed.data_ptr(), _lib.dtype_tag(x.dtype),
-                T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
-    else:
-        _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
-                x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
-                T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
+        _launch_packed(x2, packed, programs, out)
+        return out.view(*x.shape[:-1], I)
+    tiles = -(-T // 16)
+    ws = _SCRATCH.get((programs, tiles, H, I), lambda: _workspace_bytes(programs, tiles, H, I), x.device)
+    _launch("ember_gate_up_silu", _lib.load().ember_gate_up_silu, x.device,
+            x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), _lib.dtype_tag(x.dtype),
+            T, H, I, programs, ws.data_ptr(), ws.numel() * 4, out.data_ptr(), out.stride(0))
     if _check_indices():
         need, slabs = _workspace_bytes(programs, tiles, H, I), I // SLAB
         _SCRATCH.verify_counters(ws, need - round_up(slabs * 4, 256), need - round_up(slabs * 4, 256) + slabs * 4)

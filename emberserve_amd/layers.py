@@ -50,7 +50,11 @@ class SwiGLUMLP(nn.Module):
     `pack_weights()`, called once after the weights are loaded, adds a packed copy of
     gate_up_proj's weight (the same number of bytes again, outside the state dict) that the
     decode kernel streams faster; the copy is dropped when the weight tensor is replaced or
-    modified in place, and the forward then reads the weight itself."""
+    modified in place, and the forward then reads the weight itself.
+    `pack_weights(keep_weight=False)` instead replaces the weight by its packed copy: the
+    module then holds one copy of the gate_up weight (gate_up_proj.weight becomes an empty
+    tensor) and every batch runs on the packed copy, the decode kernel up to 64 tokens and
+    the packed prefill GEMM above. Load checkpoints before dropping the weight."""
 
     def __init__(self, hidden_size: int, intermediate_size: int) -> None:
         super().__init__()
@@ -65,14 +69,23 @@ class SwiGLUMLP(nn.Module):
         return (w.data_ptr(), w._version)
 
     @torch.no_grad()
-    def pack_weights(self, num_workgroups: int | None = None) -> None:
+    def pack_weights(self, num_workgroups: int | None = None, keep_weight: bool = True) -> None:
         from .gate_up_silu import pack_gate_up_weight
-        self._packed = pack_gate_up_weight(self.gate_up_proj.weight.detach(), num_workgroups)
-        self._packed_of = self._weight_key()
+        if self._packed_of == "only":
+            raise RuntimeError("SwiGLUMLP.pack_weights: the unpacked weight was already dropped")
+        w = self.gate_up_proj.weight
+        self._packed = pack_gate_up_weight(w.detach(), num_workgroups)
+        if keep_weight:
+            self._packed_of = self._weight_key()
+        else:
+            self.gate_up_proj.weight = nn.Parameter(w.new_empty(0), requires_grad=False)
+            self._packed_of = "only"  # w is freed with its last reference: stream-ordered after the packing
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         from .gate_up_silu import gate_up_silu
         packed = self._packed
+        if self._packed_of == "only":
+            return self.down_proj(gate_up_silu(x, None, packed=packed))
         if packed is not None and self._packed_of != self._weight_key():
             self._packed = self._packed_of = packed = None
         return self.down_proj(gate_up_silu(x, self.gate_up_proj.weight, packed=packed))

@@ -54,7 +54,7 @@
  *   ember_gate_up_silu_packed the same over a weight packed at load time
  *                             (ember_gate_up_silu_pack_weight); up to 64 tokens
  *   ember_gate_up_silu_gemm   the same at prefill sizes: an MFMA GEMM with the activation
- *                             in its epilogue
+ *                             in its epilogue (also _packed: over the packed weight)
  *   ember_moe_gate_up_silu    the routed experts' grouped gate_up GEMM + silu_and_mul of
  *                             fused_moe_forward, emberserve/model/moe_triton.py:332-345
  *                             (also _packed, _direct for decode batches, _gemm at prefill)
@@ -515,6 +515,18 @@ int ember_gate_up_silu_pack_weight(const void* w, int64_t w_row_stride, int dtyp
 int ember_gate_up_silu_packed(const void* x, int64_t x_row_stride, const void* packed_w, int dtype, int64_t tokens,
                               int64_t hidden, int64_t inter, int64_t num_workgroups, void* workspace,
                               int64_t workspace_bytes, void* out, int64_t out_row_stride, void* stream);
+
+/* ember_gate_up_silu_gemm over a weight packed by ember_gate_up_silu_pack_weight for
+ * num_workgroups decode workgroups: the same tiles without the 96-column one ((256, 64),
+ * (256, 128), (128, 128); inter a multiple of column_tile), the same results bit for bit.
+ * Each tile's weight operand is its 64-row slabs' packed 16 KiB units, read as contiguous
+ * 1 KiB blocks. With it a model keeps one copy of the gate_up weight (the packed one) for
+ * both the decode kernels and prefill. Replaces qwen2.py:60-61 (gate_up_proj, then
+ * silu_and_mul); num_workgroups must be the value the weight was packed for. */
+int ember_gate_up_silu_gemm_packed(const void* x, int64_t x_row_stride, const void* packed, int dtype,
+                                   int64_t tokens, int64_t hidden, int64_t inter, int64_t num_workgroups,
+                                   int64_t token_tile, int64_t column_tile, void* out, int64_t out_row_stride,
+                                   void* stream);
 
 /* Bytes of workspace ember_moe_gate_up_silu needs for num_splits > 1 (0 for one split), -1
  * for invalid arguments: fp32 partials [num_splits][num_valid][2 inter] and one uint32

@@ -287,6 +287,64 @@ def test_gemm_ragged_96_column_tile(inter, tokens):
             assert torch.equal(fused, got)
 
 
+@pytest.mark.parametrize("token_tile,tile", [(256, 64), (256, 128), (128, 128)])
+@pytest.mark.parametrize("programs", [76, 256, 1000])
+def test_gemm_packed_equals_the_gemm(token_tile, tile, programs):
+    """The prefill GEMM over the packed weight (packed for 76, 256 or 1000 decode workgroups:
+    runs that split slabs at different k, and more workgroups than units) gives the unpacked
+    GEMM's bits at every token (300 tokens: a partial token tile)."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_gemm_packed, pack_gate_up_weight
+    _say(f"gemm packed tile={token_tile}x{tile} programs={programs}")
+    g = torch.Generator().manual_seed(1100 + programs + tile)
+    x = (torch.randn(300, 1024, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(2 * 1280, 1024, generator=g) / 32).to(torch.bfloat16).to(DEV)
+    packed = pack_gate_up_weight(w, programs)
+    got = gate_up_silu_gemm_packed(x, packed, column_tile=tile, token_tile=token_tile)
+    want = gate_up_silu_gemm(x, w, column_tile=tile, token_tile=token_tile)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_packed_qwen3_8b_against_oracle(dtype):
+    """Qwen3-8B's MLP (H 4096, I 12288) at 777 tokens over a weight packed for the default
+    grid: equal to the unpacked GEMM, and sampled rows and columns against the oracle."""
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm, gate_up_silu_gemm_packed, pack_gate_up_weight
+    _say(f"gemm packed qwen3-8b {dtype}")
+    g = torch.Generator().manual_seed(1200)
+    x = (torch.randn(777, 4096, generator=g) * 0.5).to(dtype)
+    w = (torch.randn(2 * 12288, 4096, generator=g) / 64).to(dtype)
+    dx, dw = x.to(DEV), w.to(DEV)
+    got = gate_up_silu_gemm_packed(dx, pack_gate_up_weight(dw))
+    assert torch.equal(got.view(torch.int16), gate_up_silu_gemm(dx, dw, column_tile=128).view(torch.int16))
+    got = got.cpu()
+    cols = torch.randperm(12288, generator=g)[:128]
+    rows = torch.randperm(777, generator=g)[:64]
+    _check(got[rows][:, cols], x[rows], torch.cat([w[cols], w[12288 + cols]]), "packed gemm")
+
+
+def test_swiglu_mlp_keeps_one_weight_copy():
+    """pack_weights(keep_weight=False): the module holds only the packed copy and gives the
+    unpacked module's output bit for bit at decode sizes (the packed decode kernel) and at
+    prefill sizes (the packed GEMM against the unpacked GEMM)."""
+    from emberserve_amd import layers
+    from emberserve_amd.gate_up_silu import gate_up_silu_gemm
+    torch.manual_seed(2)
+    mlp = layers.SwiGLUMLP(1024, 1280).to(DEV, torch.bfloat16)
+    w = mlp.gate_up_proj.weight.detach().clone()
+    xs = [torch.randn(t, 1024, device=DEV, dtype=torch.bfloat16) for t in (1, 16, 64, 65, 600)]
+    with torch.no_grad():
+        mlp.pack_weights()
+        packed = mlp._packed
+        want = {x.shape[0]: mlp.down_proj(gate_up_silu(x, w, fused=True, packed=packed) if x.shape[0] <= 64
+                                          else gate_up_silu_gemm(x, w, column_tile=64)) for x in xs}
+        mlp.pack_weights(keep_weight=False)
+        assert mlp.gate_up_proj.weight.numel() == 0 and mlp._packed is not None
+        for x in xs:
+            assert torch.equal(mlp(x), want[x.shape[0]]), x.shape[0]
+        with pytest.raises(RuntimeError):
+            mlp.pack_weights()
+
+
 def test_gemm_rejects_bad_tiles():
     from emberserve_amd.gate_up_silu import gate_up_silu_gemm
     x = torch.randn(4, 128, device=DEV).to(torch.bfloat16)
