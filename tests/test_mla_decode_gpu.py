@@ -131,6 +131,28 @@ def test_full_size_sampled_parity_at_every_split_count():
     assert _lib.read_errors() == 0
 
 
+def test_small_grids_back_to_back_split_counts():
+    """Small grids (the staged kernel) at 4 to 32 splits, merged by k_mla_merge: calls
+    alternate between split counts, batch 1 and 2, and head counts 16 and 32 (one and two
+    chunks), with no synchronisation in between, and every call must match the oracle
+    (splits past the context publish empty partials)."""
+    cases = []
+    for heads, ctx_lens in ((16, [320]), (16, [333, 17]), (32, [320])):
+        q, lat, bt, ctx = gen.mla_decode_inputs(ctx_lens, heads, DL, DR, 16, torch.bfloat16, seed=20 + heads)
+        cases.append((heads, ctx_lens, q, lat, bt, ctx, tuple(t.to(DEV) for t in (q, lat, bt, ctx))))
+    outs = []
+    for rnd in range(2):
+        for splits in (4, 6, 8, 10, 16, 20, 32):
+            for heads, ctx_lens, q, lat, bt, ctx, dev_in in cases:
+                outs.append((heads, ctx_lens, splits, q, lat, bt, ctx,
+                             mla_decode(*dev_in[:2], dev_in[2], dev_in[3], SCALE, DL, num_splits=splits)))
+    torch.cuda.synchronize()
+    for heads, ctx_lens, splits, q, lat, bt, ctx, got in outs:
+        _check(got, q[..., :DL], q[..., DL:], lat, bt, ctx, SCALE, DL, True,
+               f"spread merge heads {heads} ctx {ctx_lens} splits {splits}")
+    assert _lib.read_errors() == 0
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3])
 def test_interpreter_geometry_fp32(splits):
     """tests/test_mla_triton.py's geometry (H 4, DL 32, DR 16, fp32), its contexts and split
