@@ -465,7 +465,7 @@ def _ops(torch, ops, tables):
         blocks + the MFMA GEMM with the activation in its epilogue) beside the 16-block kernel of the
         reference's structure (moe_triton.py:332-340: 16-row blocks of one expert). Alignment
         is launched in both. MFMA-bound: 2·N·k·2I·H flops; bytes as in the decode rows."""
-        from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu
+        from emberserve_amd.moe import fused_moe_gate_up, moe_align, moe_gate_up_silu, pack_moe_gate_up_weight
         h, inter, ne, k = 2048, 1408, 64, 6
         seed(350 + n)
         ids = torch.stack([torch.randperm(ne, generator=gi).to(dev)[:k] for _ in range(n)])
@@ -479,6 +479,13 @@ def _ops(torch, ops, tables):
         rows = 128 if n * k < 24576 else 256
         out.append(Op("moe_gate_up_silu_gemm", cfg, shape + f" (fused_moe_gate_up: align {rows} + MFMA GEMM)", nbytes,
                       make, lambda a: fused_moe_gate_up(a[0], ids, a[1]), wbytes, flops=flops))
+
+        def make_packed(i):  # the experts packed once, at load time, outside the timed region
+            x, w = make(i)
+            return x, w, pack_moe_gate_up_weight(w)
+        out.append(Op("moe_gate_up_silu_gemm_packed", cfg,
+                      shape + f" (fused_moe_gate_up over packed experts: align {rows} + MFMA GEMM)", nbytes,
+                      make_packed, lambda a: fused_moe_gate_up(a[0], ids, a[1], packed=a[2]), wbytes, flops=flops))
         out.append(Op("moe_align+gate_up_silu", cfg, shape + " (align 16 + 16-block kernel)", nbytes, make,
                       lambda a: moe_gate_up_silu(a[0], a[1], *moe_align(ids, ne), k), wbytes, flops=flops))
 

@@ -76,6 +76,8 @@ SIGNATURES: dict[str, list] = {
                                     _i64, _i64, _p, _i64, _p],
     "ember_gate_up_silu_packed": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _p],
     "ember_gate_up_silu_gemm_packed": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "ember_moe_gate_up_silu_gemm_packed": [_p, _i64, _i64, _p, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64,
+                                           _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu": [_p, _i64, _i64, _p, _i64, _i64, _i32, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
                                _i64, _p, _i64, _p, _i64, _p],
     "ember_moe_gate_up_silu_workspace_bytes": [_i64, _i64, _i64, _i64],

@@ -161,7 +161,6 @@ struct PackedSlabWalk {
 template <typename T, int BNG, int BM, bool MOE, bool PK = false>
 __global__ void __launch_bounds__(512, 1)
 k_gate_up_silu_gemm(GemmArgs a) {
-  static_assert(!(MOE && PK), "packed weights are dense only");
   static_assert(!PK || BNG % 64 == 0, "packed tiles are whole 64-row slabs");
   using M = GemmMfma<T>;
   using V8 = typename M::v8;
@@ -193,14 +192,30 @@ k_gate_up_silu_gemm(GemmArgs a) {
   const int n = lane & 15, g = lane >> 4;
 
   // XCD-aware tile order, then GROUP_M token tiles per band of column tiles
-  const int mtiles = (a.T + BM - 1) / BM;
+  int mtiles = (a.T + BM - 1) / BM;
   const int ntiles = (a.I + BNG - 1) / BNG;  // the last one ragged when BNG does not divide I
   int pid = blockIdx.x;
+  int nb = gridDim.x;
+  if (MOE) {
+    // The grid covers every block the layout may use, but only the blocks before the first
+    // one past the last expert hold work (block_expert is ascending, num_experts after the
+    // used blocks). Counted here (one coalesced read of the small table, the same for every
+    // workgroup) so that the XCD ranges below split the real tiles evenly instead of
+    // leaving the unused blocks' share of the chip idle.
+    int used = 0;
+    for (int i0 = 0; i0 < mtiles; i0 += kWave) {
+      const int i = i0 + lane;
+      const bool u = i < mtiles && a.block_expert[i] < a.E;
+      used += __builtin_popcountll(__ballot(u));
+    }
+    mtiles = used;
+    nb = used * ntiles;
+  }
   {
-    const int nb = gridDim.x;
     const int per = (nb + 7) / 8;
     const int xcd = pid % 8, idx = pid / 8;
     const int full = nb % 8 == 0 ? 8 : nb % 8;
+    if (MOE && idx >= (xcd < full ? per : per - 1)) return;  // past this XCD's share of the real tiles
     pid = xcd < full ? xcd * per + idx : full * per + (xcd - full) * (per - 1) + idx;
   }
   constexpr int GM = EMBER_GEMM_GROUP_M;
@@ -271,18 +286,26 @@ k_gate_up_silu_gemm(GemmArgs a) {
     }
   }
   const int nd = a.H / 64;  // double stages
+  // Dense packed weights: a unit's place depends on the decode grid it was packed for, so
+  // each slab's units are walked in k order. Routed experts' packed weights are per expert
+  // k-major (unit j * slabs + slab of the expert's array), so a stage's S units are adjacent.
   PackedSlabWalk walk[S];
-  if (PK) {
+  if (PK && !MOE) {
 #pragma unroll
     for (int ss = 0; ss < S; ++ss) walk[ss].init(n0 / 64 + ss, nd, a.pk_total, a.pk_G);
   }
-  // element offsets of this double stage's weight units (PK); the walks then move on
+  // element offsets of double stage d's weight units (PK)
   int64_t wofs[S];
-  auto next_units = [&]() {
+  auto next_units = [&](int d) {
+    constexpr int64_t kUnitElems = 16384 / static_cast<int64_t>(sizeof(T));
 #pragma unroll
     for (int ss = 0; ss < S; ++ss) {
-      wofs[ss] = walk[ss].template elem_offset<T>();
-      walk[ss].advance();
+      if (MOE) {
+        wofs[ss] = (static_cast<int64_t>(min(d, nd - 1)) * (a.I / 64) + n0 / 64 + ss) * kUnitElems;
+      } else {
+        wofs[ss] = walk[ss].template elem_offset<T>();
+        walk[ss].advance();
+      }
     }
   };
   auto wk = [&](int i, int kk) -> int64_t { return PK ? wofs[wsl[i]] : kk; };
@@ -290,14 +313,14 @@ k_gate_up_silu_gemm(GemmArgs a) {
   auto xbuf = [&](int d) { return lds + (SPLIT ? 3 * WREG + (d % 2) * XREG : (d % NBUF) * DST + WREG); };
   auto issue = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
-    if (PK) next_units();
+    if (PK) next_units(d);
     unsigned char* st = lds + (d % NBUF) * DST;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) gemm_load_lds16(src[i] + (isw[i] ? wk(i, kk) : kk), st + dst[i]);
   };
   auto issue_w = [&](int d) {
     const int kk = min(d, nd - 1) * 64;
-    if (PK) next_units();
+    if (PK) next_units(d);
 #pragma unroll
     for (int i = 0; i < WL; ++i) gemm_load_lds16(src[i] + wk(i, kk), wbuf(d) + dst[i]);
   };
@@ -522,4 +545,41 @@ extern "C" int ember_gate_up_silu_gemm_packed(const void* x, int64_t x_row_strid
   if (token_tile == 128) return launch_gemm<__bf16, 128, 128, false, true>(a, st);
   return column_tile == 64 ? launch_gemm<__bf16, 64, 256, false, true>(a, st)
                            : launch_gemm<__bf16, 128, 256, false, true>(a, st);
+}
+
+extern "C" int ember_moe_gate_up_silu_gemm_packed(const void* x, int64_t x_row_stride, int64_t num_tokens,
+                                                  const void* packed, int dtype, int64_t num_experts, int64_t hidden,
+                                                  int64_t inter, const int32_t* sorted_ids,
+                                                  const int32_t* block_expert, int64_t num_blocks, int64_t block_rows,
+                                                  int64_t num_valid, int64_t top_k, int64_t column_tile, void* out,
+                                                  int64_t out_row_stride, void* stream) {
+  using namespace ember;
+  if (num_blocks == 0 || num_valid == 0) return EMBER_OK;
+  if (num_blocks < 0 || num_valid < 0 || num_tokens < 1 || top_k < 1 || num_experts < 1 || num_blocks > (1 << 22) ||
+      num_valid > INT32_MAX / 2 || num_tokens > INT32_MAX || hidden < 64 || hidden % 64 != 0 ||
+      hidden > (int64_t(1) << 20) || inter < 64 || inter > (int64_t(1) << 28))
+    return EMBER_EINVAL;
+  const bool shape = (block_rows == 256 && (column_tile == 64 || column_tile == 128)) ||
+                     (block_rows == 128 && column_tile == 128);
+  if (!shape || inter % column_tile != 0) return EMBER_EINVAL;
+  if (dtype != EMBER_F16 && dtype != EMBER_BF16) return EMBER_EINVAL;
+  if (x == nullptr || packed == nullptr || out == nullptr || sorted_ids == nullptr || block_expert == nullptr ||
+      !aligned16(x) || !aligned16(packed) || !aligned16(out))
+    return EMBER_EINVAL;
+  if (x_row_stride < hidden || out_row_stride < inter || x_row_stride % 8 != 0 || out_row_stride % 4 != 0)
+    return EMBER_EINVAL;
+  GemmArgs a{x, x_row_stride, packed, 0, out, out_row_stride, static_cast<int>(num_blocks * block_rows),
+             static_cast<int>(hidden), static_cast<int>(inter), sorted_ids, block_expert,
+             static_cast<int>(num_valid), static_cast<int>(top_k), static_cast<int>(num_experts),
+             static_cast<int>(num_tokens), 2 * inter * hidden, device_error_word(), 0, 1};
+  if (a.err == nullptr) return EMBER_ENODEV;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == EMBER_F16) {
+    if (block_rows == 128) return launch_gemm<_Float16, 128, 128, true, true>(a, st);
+    return column_tile == 64 ? launch_gemm<_Float16, 64, 256, true, true>(a, st)
+                             : launch_gemm<_Float16, 128, 256, true, true>(a, st);
+  }
+  if (block_rows == 128) return launch_gemm<__bf16, 128, 128, true, true>(a, st);
+  return column_tile == 64 ? launch_gemm<__bf16, 64, 256, true, true>(a, st)
+                           : launch_gemm<__bf16, 128, 256, true, true>(a, st);
 }

@@ -275,21 +275,31 @@ GEMM_WIDE_FROM = 24576
 PACKED_MAX_ASSIGNMENTS = 768
 
 
-def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, column_tile: int = 128,
-                          block_rows: int = GEMM_BLOCK_M) -> Tensor:
+def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor | None, topk_ids: Tensor, *, column_tile: int = 128,
+                          block_rows: int = GEMM_BLOCK_M, packed: PackedExperts | None = None) -> Tensor:
     """act [N * k, I] at prefill sizes (`ember_moe_gate_up_silu_gemm`): moe_align with
     block_rows-row blocks (256, or 128 with 128-column tiles), then the MFMA GEMM of
     `gate_up_silu_gemm` with one block per token tile over the block's gathered x
     rows and its expert's weight, silu_and_mul in the epilogue, rows scattered back to
     assignment order. The first grouped GEMM + silu_and_mul of moe_triton.py:339-340;
-    bit-identical to `moe_gate_up_silu` for every assignment."""
-    assert x.dim() == 2 and w_gate_up.dim() == 3 and topk_ids.dim() == 2, (x.shape, w_gate_up.shape, topk_ids.shape)
-    _require_device("moe_gate_up_silu_gemm", x, w_gate_up, topk_ids)
-    E, two_i, H = w_gate_up.shape
+    bit-identical to `moe_gate_up_silu` for every assignment. With `packed`
+    (`pack_moe_gate_up_weight`) the GEMM reads the packed experts
+    (`ember_moe_gate_up_silu_gemm_packed`: contiguous 16 KiB units per stage, the same
+    bits) and w_gate_up may be None."""
+    assert x.dim() == 2 and topk_ids.dim() == 2, (x.shape, topk_ids.shape)
+    if packed is not None:
+        E, two_i, H = packed.num_experts, 2 * packed.inter, packed.hidden
+        _require_device("moe_gate_up_silu_gemm", x, packed.packed, topk_ids)
+        wdtype = packed.dtype
+    else:
+        assert w_gate_up is not None and w_gate_up.dim() == 3, "moe_gate_up_silu_gemm: w_gate_up or packed"
+        _require_device("moe_gate_up_silu_gemm", x, w_gate_up, topk_ids)
+        E, two_i, H = w_gate_up.shape
+        wdtype = w_gate_up.dtype
     inter = two_i // 2
     n, k = topk_ids.shape
     if x.shape[1] != H or two_i % 2 or n > x.shape[0]:
-        raise ValueError(f"moe_gate_up_silu_gemm: x {tuple(x.shape)}, w_gate_up {tuple(w_gate_up.shape)} and "
+        raise ValueError(f"moe_gate_up_silu_gemm: x {tuple(x.shape)}, weights [{E}, {two_i}, {H}] and "
                          f"topk_ids {tuple(topk_ids.shape)} do not match")
     if (block_rows, column_tile) not in ((256, 64), (256, 128), (128, 128)):
         raise ValueError(f"moe_gate_up_silu_gemm: no ({block_rows}, {column_tile}) tile")
@@ -297,17 +307,24 @@ def moe_gate_up_silu_gemm(x: Tensor, w_gate_up: Tensor, topk_ids: Tensor, *, col
     out = torch.empty((num_valid, inter), dtype=x.dtype, device=x.device)
     if num_valid == 0:
         return out
-    fits = (x.dtype == w_gate_up.dtype and x.dtype in SUPPORTED_DTYPES and H % 64 == 0
-            and inter % column_tile == 0 and x.stride(1) == 1 and w_gate_up.stride(2) == 1
-            and x.stride(0) % 8 == 0 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
-            and x.data_ptr() % 16 == 0 and w_gate_up.data_ptr() % 16 == 0)
+    fits = (x.dtype == wdtype and x.dtype in SUPPORTED_DTYPES and H % 64 == 0
+            and inter % column_tile == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0)
+    if packed is None:
+        fits = fits and (w_gate_up.stride(2) == 1 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
+                         and w_gate_up.data_ptr() % 16 == 0)
     if not fits:
         raise ValueError(f"moe_gate_up_silu_gemm: shape, dtype or alignment not supported (H {H}, I {inter}, "
                          f"column_tile {column_tile}, {x.dtype})")
-    _launch("ember_moe_gate_up_silu_gemm", _lib.load().ember_moe_gate_up_silu_gemm, x.device,
-            x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
-            _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
-            block_expert.numel(), block_rows, num_valid, k, column_tile, out.data_ptr(), out.stride(0))
+    if packed is not None:
+        _launch("ember_moe_gate_up_silu_gemm_packed", _lib.load().ember_moe_gate_up_silu_gemm_packed, x.device,
+                x.data_ptr(), x.stride(0), x.shape[0], packed.packed.data_ptr(), _lib.dtype_tag(x.dtype), E, H, inter,
+                sorted_ids.data_ptr(), block_expert.data_ptr(), block_expert.numel(), block_rows, num_valid, k,
+                column_tile, out.data_ptr(), out.stride(0))
+    else:
+        _launch("ember_moe_gate_up_silu_gemm", _lib.load().ember_moe_gate_up_silu_gemm, x.device,
+                x.data_ptr(), x.stride(0), x.shape[0], w_gate_up.data_ptr(), w_gate_up.stride(0), w_gate_up.stride(1),
+                _lib.dtype_tag(x.dtype), E, H, inter, sorted_ids.data_ptr(), block_expert.data_ptr(),
+                block_expert.numel(), block_rows, num_valid, k, column_tile, out.data_ptr(), out.stride(0))
     if _check_indices() and _lib.read_errors(clear=True) & _lib.ERR_ROW_INDEX:
         raise IndexError("emberserve_amd.moe_gate_up_silu_gemm: assignment id past the token rows")
     return out
@@ -360,10 +377,11 @@ def fused_moe_gate_up(x: Tensor, topk_ids: Tensor, w_gate_up: Tensor, *, num_spl
             and x.dtype in SUPPORTED_DTYPES and H % 64 == 0 and (two_i // 2) % 64 == 0
             and w_gate_up.stride(2) == 1 and w_gate_up.stride(1) % 8 == 0 and w_gate_up.stride(0) % 8 == 0
             and w_gate_up.data_ptr() % 16 == 0):
+        # over the packed experts when there are (contiguous units; the same bits)
         if (two_i // 2) % 128 == 0:
             rows = 128 if n * k < GEMM_WIDE_FROM else 256
-            return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=128, block_rows=rows)
-        return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=64, block_rows=256)
+            return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=128, block_rows=rows, packed=packed)
+        return moe_gate_up_silu_gemm(x, w_gate_up, topk_ids, column_tile=64, block_rows=256, packed=packed)
     if packed is not None and n * k > PACKED_MAX_ASSIGNMENTS:
         packed = None  # the row kernel is faster there (see PACKED_MAX_ASSIGNMENTS)
     sorted_ids, block_expert, num_valid = moe_align(topk_ids, E)

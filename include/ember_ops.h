@@ -528,6 +528,17 @@ int ember_gate_up_silu_gemm_packed(const void* x, int64_t x_row_stride, const vo
                                    int64_t token_tile, int64_t column_tile, void* out, int64_t out_row_stride,
                                    void* stream);
 
+/* ember_moe_gate_up_silu_gemm over experts packed by ember_moe_gate_up_silu_pack_weight
+ * (tiles (256, 64), (256, 128), (128, 128); inter a multiple of column_tile): the same
+ * results bit for bit. Each stage of a tile reads its slabs' adjacent 16 KiB units of the
+ * expert's k-major packed array, contiguous memory instead of 128-byte pieces of 256
+ * weight rows. Replaces the same reference calls (moe_triton.py:307-329, :339-340). */
+int ember_moe_gate_up_silu_gemm_packed(const void* x, int64_t x_row_stride, int64_t num_tokens, const void* packed,
+                                       int dtype, int64_t num_experts, int64_t hidden, int64_t inter,
+                                       const int32_t* sorted_ids, const int32_t* block_expert, int64_t num_blocks,
+                                       int64_t block_rows, int64_t num_valid, int64_t top_k, int64_t column_tile,
+                                       void* out, int64_t out_row_stride, void* stream);
+
 /* Bytes of workspace ember_moe_gate_up_silu needs for num_splits > 1 (0 for one split), -1
  * for invalid arguments: fp32 partials [num_splits][num_valid][2 inter] and one uint32
  * arrival counter per (block, 64-column slab). */

@@ -268,9 +268,13 @@ def test_moe_gemm_equals_the_row_kernel(n, experts, skew):
     ids = ids.to(DEV)
     si, be, nv = moe_align(ids, experts)
     want = moe_gate_up_silu(x, w, si, be, nv, K, num_splits=1)
+    packed = pack_moe_gate_up_weight(w)
     for rows, tile in ((256, 64), (256, 128), (128, 128)):
         got = moe_gate_up_silu_gemm(x, w, ids, column_tile=tile, block_rows=rows)
         assert torch.equal(got, want), (rows, tile)
+        # over the packed experts (ember_moe_gate_up_silu_gemm_packed), no unpacked weight
+        got = moe_gate_up_silu_gemm(x, None, ids, column_tile=tile, block_rows=rows, packed=packed)
+        assert torch.equal(got, want), ("packed", rows, tile)
 
 
 def test_fused_moe_gate_up_takes_the_gemm_at_prefill_sizes(monkeypatch):
