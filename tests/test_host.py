@@ -434,6 +434,39 @@ def test_gate_up_silu_abi_validation():
     assert call() == 1  # null pointers
 
 
+def test_packed_gemm_abi_validation():
+    """The packed prefill GEMMs reject bad shapes and tiles (no 96-column tile: slabs are
+    64 rows) before any device call."""
+    lib = _lib.load()
+
+    def dense(tokens=300, hidden=4096, inter=12288, programs=256, rows=256, tile=128, dtype=2):
+        return lib.ember_gate_up_silu_gemm_packed(None, hidden, None, dtype, tokens, hidden, inter, programs, rows, tile,
+                                                  None, inter, None)
+    assert dense(tokens=0) == 0
+    for bad in (dict(tile=96), dict(rows=128, tile=64), dict(inter=4864 + 64), dict(hidden=100), dict(programs=0),
+                dict(dtype=0), dict(tokens=-1)):
+        assert dense(**bad) == 1, bad
+    assert dense() == 1  # null pointers
+
+    def moe(blocks=4, rows=256, valid=10, tokens=5, top_k=2, experts=8, hidden=2048, inter=1408, tile=64, dtype=2):
+        return lib.ember_moe_gate_up_silu_gemm_packed(None, hidden, tokens, None, dtype, experts, hidden, inter, None,
+                                                      None, blocks, rows, valid, top_k, tile, None, inter, None)
+    assert moe(blocks=0) == 0 and moe(valid=0) == 0
+    for bad in (dict(tile=96), dict(rows=128, tile=64), dict(tile=128, inter=1344), dict(top_k=0), dict(dtype=0)):
+        assert moe(**bad) == 1, bad
+    assert moe() == 1
+
+
+def test_gate_up_silu_without_the_unpacked_weight():
+    """weight None needs the packed copy, and cannot take the unfused pair."""
+    from emberserve_amd.gate_up_silu import gate_up_silu
+    x = torch.zeros(4, 64)
+    with pytest.raises(ValueError):
+        gate_up_silu(x, None)
+    with pytest.raises(ValueError):
+        gate_up_silu(x, None, packed=object(), fused=False)
+
+
 # ---- MoE gate_up + silu_and_mul (host side) -------------------------------------------------
 @pytest.mark.parametrize("n,e,k", [(1, 64, 6), (7, 8, 2), (50, 16, 4), (3, 4, 4)])
 def test_moe_align_layout(n, e, k):
