@@ -994,6 +994,9 @@ def main() -> int:
     traffic = _profiled_traffic("add_rmsnorm_T8192_bytes")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
+                "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this kernel, scaled by a 256 MiB "
+                                  "copy's readings (profiles/add_rmsnorm_T8192_traffic.md); counters cannot be "
+                                  "read inside this process",
                 "kernel": "k_rmsnorm<bf16, RESID> (fused residual add + RMSNorm), [8192, 4096] bf16",
                 "bytes_per_launch": add_bytes, "avg_launch_us": round(add_us, 2)}
     torch.cuda.empty_cache()
