@@ -136,11 +136,13 @@ class SegmentGraphs:
         return bool(self._graphs)
 
     # --------------------------------------------------------------------- capture
-    @torch.inference_mode()
     def capture(self, warmup: int = 1) -> None:
         """Records every (bucket, segment) graph, largest bucket first. Each bucket's
         segments run `warmup` times eagerly on the capture stream before they are
-        recorded (first-call work such as library handle set-up stays out of the graph)."""
+        recorded (first-call work such as library handle set-up stays out of the graph).
+        Runs in the caller's grad mode: call it under `torch.inference_mode()` when the
+        pieces need it (capturing inside inference mode makes torch's graph RNG state an
+        inference tensor, which a later capture outside it cannot update)."""
         if self.device.type != "cuda":
             for t in self.buckets:
                 self._graphs[t] = [(lambda s=s, t=t: self._segment(s, t)) for s in range(self.num_segments)]
@@ -194,7 +196,6 @@ class SegmentGraphs:
                 attend(s, n)
         return t
 
-    @torch.inference_mode()
     def release(self) -> None:
         """Drops every graph (and with them the pool's memory)."""
         self._graphs.clear()
