@@ -15,7 +15,9 @@ Printed before the JSON line, one short `row cfg=...` line each (and in full wit
 Also in the JSON line:
   us_per_layer  config 4 summed per T, plus the full per-layer elementwise set
   graph_replay  the Qwen3-8B per-layer kernels of all 36 layers recorded in one hipGraph
-                (torch.cuda.graph) and replayed, against eager launches (wall us per layer)
+                (torch.cuda.graph) and replayed, against eager launches (wall us per layer);
+                and a 36-layer step through the padded-bucket segment graphs (L + 1
+                graphs) against one graph per (layer, piece) (wall us per step)
   roofline      the dominant kernel of the step (add+RMSNorm, T=8192), timed live with
                 hipEvents around back-to-back launches on its launch stream
   cpu_baseline  the CPU oracle (the reference's PyTorch-eager ops restated) on a bounded
@@ -726,7 +728,74 @@ def _graph_replay(torch, ops, tables, layers=36, reps=20):
         del graph
         torch.cuda.empty_cache()
     out.update(_graph_decode_step(torch, ops, tables, layers=layers, reps=reps))
+    out.update(_segment_graphs(torch, ops, layers=layers, reps=reps))
     return out
+
+
+def _segment_graphs(torch, ops, layers=36, reps=20, bucket=16, n=9):
+    """A prefill/mixed step through the padded-bucket runner (emberserve_amd.piecewise):
+    the L + 1 segment graphs of SegmentGraphs against one graph per (layer, piece), the
+    structure of the reference's runner (piecewise_graphs.py), for 36 layers at bucket 16
+    with 9 real rows. Pieces: pre = add + RMSNorm; post = silu_and_mul + a row copy; the
+    eager attention between them is a stand-in add. Wall µs per step."""
+    from emberserve_amd.piecewise import SegmentGraphs
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    hid = torch.randn((bucket, 4096), generator=g, device=dev).to(bf)
+    res = torch.randn((bucket, 4096), generator=g, device=dev).to(bf)
+    nrm = torch.empty_like(hid)
+    gu = torch.randn((bucket, 2 * 12288), generator=g, device=dev).to(bf)
+    act = torch.empty((bucket, 12288), device=dev, dtype=bf)
+    w = (torch.randn(4096, generator=g, device=dev) * 0.1 + 1).to(bf)
+
+    def pre(i, t):
+        ops.fused_add_rmsnorm_hip(hid[:t], res[:t], w, 1e-6, out=nrm[:t], residual_out=res[:t])
+
+    def post(i, t):
+        ops.silu_and_mul_hip(gu[:t], out=act[:t])
+        hid[:t].copy_(act[:t, :4096])
+
+    def attend(i, rows):
+        hid[:rows].add_(nrm[:rows])
+
+    sg = SegmentGraphs(layers, (bucket,), pre, post, dev)
+    sg.capture()
+    pool = torch.cuda.graph_pool_handle()
+    cap = torch.cuda.Stream()
+    pieces = []
+    for i in range(layers):
+        for f in (pre, post):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, pool=pool, stream=cap):
+                f(i, bucket)
+            pieces.append(gr)
+
+    def per_piece():
+        for i in range(layers):
+            pieces[2 * i].replay()
+            attend(i, n)
+            pieces[2 * i + 1].replay()
+
+    def wall(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    seg_us = wall(lambda: sg.step(n, attend)) * 1e6
+    piece_us = wall(per_piece) * 1e6
+    sg.release()
+    del pieces
+    torch.cuda.empty_cache()
+    return {f"segment_graphs_{layers}L_bucket{bucket}": {
+        "segment_graphs_us_per_step": round(seg_us, 1), "graphs_per_step": layers + 1,
+        "per_piece_graphs_us_per_step": round(piece_us, 1), "per_piece_graphs_per_step": 2 * layers}}
 
 
 def _graph_decode_step(torch, ops, tables, layers=36, reps=10, batch=64, ctx=2048):
