@@ -386,7 +386,16 @@ k_gate_up_silu_gemm(GemmArgs a) {
     if (!even) gemm_wait_vm<kNextLanded>();  // the next double stage has landed
     gemm_wait_lgkm0();
   };
+  // Routed experts: an expert's run is padded to whole blocks at its end, so a wave whose
+  // 64 rows start with a padding assignment holds padding only; it still loads its share
+  // of the tiles and keeps the barriers, but skips the MFMAs (nothing of it is stored).
+  bool live = true;
+  if (MOE) {
+    const int id0 = a.sorted_ids[m0 + 64 * q];
+    live = __builtin_amdgcn_readfirstlane(id0 >= 0 && id0 < a.num_valid ? 1 : 0) != 0;
+  }
   auto cphase = [&]() {
+    if (MOE && !live) return;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
